@@ -1,0 +1,190 @@
+"""Attention throughput on one MI355X: the BASELINE metric (attention TFLOP/s and % of the int8 MFMA peak at
+H=32, D=128, S=16896; ms per call).
+
+    python bench.py [--gpus 1] [--steps 20] [--warmup 3] [--config c4] [--no-cpu]
+
+A step is one attention call over the whole workload (all heads, all query rows) with its inputs resident in
+HBM. The default workload is BASELINE config 4: B=1, H=32, D=128, S=16896 (512 text + 16384 image rows), Q/K bf16
+~N(0,1) with 4 of 128 channels per head x20, rotated and quantised to int8 by the fused pre-pass (timed
+separately, reported under "prepass"), V bf16 ~N(0,1), int8 QK^T + bf16 P V. FLOPs follow the reference's
+convention 4*H*Sq*Sk_valid*D (bench/attn_bench.py:27). The timed region is bracketed by stream
+synchronisations; GPU time comes from HIP events on the library's stream (h3_wait), per-launch durations from
+per-dispatch event pairs (profile mode). One JSON line is printed.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+PEAK = {"int8": 5.0e15, "bf16": 2.5e15}  # MI355X dense MFMA peaks (ops/s)
+HBM_PEAK = 8.0e12
+
+CONFIGS = {
+    # name: (H, D, S, L (valid keys), path)
+    "c1": (4, 128, 256, 256, "bf16"),
+    "c2": (24, 128, 4608, 4608, "bf16"),
+    "c3": (30, 128, 4608, None, "bf16"),
+    "c4": (32, 128, 16896, 16896, "int8"),
+    "c5": (32, 128, 66048, 66048, "int8"),
+}
+
+
+def make_inputs(gpu, cfg, rng):
+    """Device-resident inputs of one config. Returns (kwargs for ops.attention, prepass closure or None, L)."""
+    from h3metal_amd import ops
+    from oracle.bf16 import to_bf16  # bf16 rounding of the synthetic host data only
+    H, D, S, L, path = CONFIGS[cfg]
+    if L is None:  # config 3: 4096 image rows, text padded to 512 with L_txt ~ U[32, 512] valid
+        L = 4096 + int(rng.integers(32, 513))
+    if path == "int8":
+        X = gpu.empty((S, 3 * H * D), "bf16")
+        chunk = 2048
+        for r0 in range(0, S, chunk):  # generate in row chunks to bound host memory
+            n = min(chunk, S - r0)
+            x = rng.standard_normal((n, 3, H, D), dtype=np.float32)
+            if r0 == 0:
+                out_ch = [rng.choice(D, 4, replace=False) for _ in range(2 * H)]
+            for part in (0, 1):
+                for h in range(H):
+                    x[:, part, h, out_ch[part * H + h]] *= 20
+            X.write(to_bf16(x.reshape(n, -1)), offset_elems=r0 * 3 * H * D)
+        Q, K = gpu.empty((H, S, D), "i8"), gpu.empty((H, S, D), "i8")
+        V = gpu.empty((H, S, D), "bf16")
+        qs, ks = gpu.empty((H, S), "f32"), gpu.empty((H, S), "f32")
+
+        def prepass():
+            ops.qk_norm_rope(gpu, X, None, None, None, None, Q, K, V, M=S, Hq=H, Hk=H, Hv=H, hd=D, out_rows=S,
+                             rot=0, eps=1e-6, norm=False, q_scale=qs, k_scale=ks, qk_rot=True)
+        prepass()
+        gpu.wait()
+        kw = dict(q=Q, k=K, v=V, q_scale=qs, k_scale=ks)
+        return kw, prepass, L
+    Q, K, V = (gpu.empty((H, S, D), "bf16") for _ in range(3))
+    for t in (Q, K, V):
+        for h in range(H):
+            t.write(to_bf16(rng.standard_normal((S, D), dtype=np.float32)), offset_elems=h * S * D)
+    return dict(q=Q, k=K, v=V), None, L
+
+
+def cpu_baseline(cfg, L, budget_s=20.0):
+    """The oracle's float32 numpy attention (query-chunked) of one head at the config's full size, timed on this
+    host, extrapolated linearly in H to the whole call. Heads are timed until ~budget_s seconds are spent."""
+    from oracle.attention import attention_f32_chunked
+    H, D, S, _, _ = CONFIGS[cfg]
+    rng = np.random.default_rng(7)
+    q, k, v = (rng.standard_normal((n, D), dtype=np.float32) for n in (S, L, L))
+    times = []
+    t_start = time.perf_counter()
+    while len(times) < H and (not times or time.perf_counter() - t_start < budget_s):
+        t0 = time.perf_counter()
+        attention_f32_chunked(q, k, v, D ** -0.5, chunk=512)
+        times.append(time.perf_counter() - t0)
+    per_head = float(np.median(times))
+    total = per_head * H
+    threads = None
+    try:
+        from threadpoolctl import threadpool_info
+        info = threadpool_info()
+        threads = max((i.get("num_threads") or 0) for i in info) if info else None
+    except Exception:  # noqa: BLE001
+        pass
+    return {"value": round(4.0 * H * S * L * D / total / 1e12, 4), "unit": "TFLOP/s",
+            "cores": threads or os.cpu_count(), "kind": "port",
+            "sample": f"{len(times)} of {H} heads at full size (Sq={S}, Sk={L}, D={D}), float32 numpy "
+                      f"(BLAS sgemm + exp, 512-row query chunks), median head time {per_head:.3f} s, "
+                      f"extrapolated x{H} heads = {total:.2f} s per call"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=int(os.environ.get("WORLD_SIZE", "1")))
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--config", default="c4", choices=sorted(CONFIGS))
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--cpu-budget", type=float, default=20.0)
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU: this build runs the attention path on a single MI355X (no multi-GPU "
+              f"path), so --gpus {args.gpus} is not supported", file=sys.stderr)
+        sys.exit(2)
+
+    from h3metal_amd import ops
+    from h3metal_amd.gpu import Gpu
+
+    H, D, S, _, path = CONFIGS[args.config]
+    gpu = Gpu()
+    rng = np.random.default_rng(0)
+    kw, prepass, L = make_inputs(gpu, args.config, rng)
+    O = gpu.empty((S, H * D), "bf16")
+
+    def step():
+        ops.attention(gpu, kw["q"], kw["k"], kw["v"], O, Lq=S, L=L, H=H, KVH=H, D=D, q_rows=S, k_rows=S,
+                      scale=D ** -0.5, q_scale=kw.get("q_scale"), k_scale=kw.get("k_scale"))
+
+    for _ in range(args.warmup):
+        step()
+    gpu.wait()
+    # timed region: the stream is drained on both sides; GPU time from HIP events on the library's stream
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    gpu_s = gpu.wait()
+    wall_s = time.perf_counter() - t0
+    # per-launch durations (event pair per dispatch) for the roofline
+    gpu.profile(True)
+    for _ in range(args.steps):
+        step()
+    gpu.wait()
+    launches = [t for _, t in gpu.profile_take()]
+    gpu.profile(False)
+    per_launch = float(np.mean(launches))
+    flops = 4.0 * H * S * L * D
+    ms = gpu_s / args.steps * 1e3
+    value = flops / (gpu_s / args.steps) / 1e12
+    peak = PEAK["int8" if path == "int8" else "bf16"]
+    achieved = flops / per_launch
+    out = {
+        "metric": "attention TFLOP/s (% of MI355X MFMA peak) at H=32,D=128,S=16896; ms/call",
+        "value": round(value, 2), "unit": "TFLOP/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(ms, 4), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "int8 QK^T (int32 acc) + bf16 PV (fp32 acc)" if path == "int8" else "bf16 (fp32 acc)",
+        "data": "synthetic (seeded N(0,1); config-4 outlier recipe)",
+        "config": {"workload": f"BASELINE {args.config}: B=1 H={H} D={D} Sq={S} Sk_valid={L}, non-causal, "
+                               f"{'Hadamard-rotated int8 Q/K + bf16 V' if path == 'int8' else 'bf16 Q/K/V'}",
+                   "global_batch": 1, "seq_len": S, "parallelism": "single GPU"},
+        "pct_of_peak": round(100 * value * 1e12 / peak, 2),
+        "wall_ms_per_step": round(wall_s / args.steps * 1e3, 4),
+        "roofline": {"bound": "mfma", "achieved": round(achieved / 1e12, 2), "peak": peak / 1e12,
+                     "unit": "TFLOP/s", "frac": round(achieved / peak, 4), "traffic": None,
+                     "kernel": "attention_kernel (int8 QK, bf16 PV)" if path == "int8" else "attention_kernel (bf16)",
+                     "per_launch_ms": round(per_launch * 1e3, 4)},
+    }
+    if prepass is not None:
+        gpu.profile(True)
+        for _ in range(args.steps):
+            prepass()
+        gpu.wait()
+        pt = float(np.mean([t for _, t in gpu.profile_take()]))
+        gpu.profile(False)
+        # algorithmic bytes: read Q, K, V bf16; write Q, K int8, V bf16, one fp32 scale per Q/K row
+        nbytes = S * 3 * H * D * 2 + 2 * S * H * D + S * H * D * 2 + 2 * S * H * 4
+        out["prepass"] = {"ms": round(pt * 1e3, 4), "bytes": nbytes, "GB/s": round(nbytes / pt / 1e9, 1),
+                          "frac_hbm": round(nbytes / pt / HBM_PEAK, 4)}
+    if not args.no_cpu:
+        out["cpu_baseline"] = cpu_baseline(args.config, L, args.cpu_budget)
+    gpu.close()
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,70 @@
+"""Builds libh3hip.so (the C ABI of include/h3hip.h) for gfx950 with hipcc.
+
+    python -m h3metal_amd.build
+
+Each source compiles to an object in h3metal_amd/_build/ in parallel, then one
+shared library is linked next to this file, where gpu.py loads it. Flags:
+  * --offload-arch=gfx950 only (CDNA4; no other targets),
+  * packed fp32 instructions disabled (-target-feature -packed-fp32-ops),
+  * the pre-pass without FMA contraction, so its float32 steps are the
+    separately rounded operations a CPU restatement reproduces bit for bit.
+"""
+
+from __future__ import annotations
+
+import concurrent.futures as cf
+import os
+import shutil
+import subprocess
+import sys
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+CSRC = os.path.join(HERE, "csrc")
+OUT_DIR = os.path.join(HERE, "_build")
+LIB = os.path.join(HERE, "libh3hip.so")
+
+COMMON = ["--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC", "-Wall", "-Wno-unused-function",
+          "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
+PER_FILE = {
+    "qk_prepass.hip": ["-ffp-contract=off"],
+}
+SOURCES = ["capi.hip", "attention.hip", "qk_prepass.hip"]
+
+
+def hipcc() -> str:
+    for c in (os.environ.get("HIPCC", ""), "/opt/rocm/bin/hipcc", shutil.which("hipcc") or ""):
+        if c and os.path.exists(c):
+            return c
+    raise FileNotFoundError("hipcc not found (ROCm is required to build the gfx950 kernels)")
+
+
+def _compile(src: str) -> str:
+    obj = os.path.join(OUT_DIR, src.replace(".hip", ".o"))
+    cmd = [hipcc(), *COMMON, *PER_FILE.get(src, []), "-c", os.path.join(CSRC, src), "-o", obj]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode:
+        raise RuntimeError(f"compiling {src} failed:\n{' '.join(cmd)}\n{r.stdout}{r.stderr}")
+    return obj
+
+
+def build(verbose: bool = True) -> str:
+    os.makedirs(OUT_DIR, exist_ok=True)
+    with cf.ThreadPoolExecutor(max_workers=min(len(SOURCES), os.cpu_count() or 4)) as ex:
+        objs = list(ex.map(_compile, SOURCES))
+    tmp = LIB + ".tmp"
+    cmd = [hipcc(), "--offload-arch=gfx950", "-shared", "-fPIC", *objs, "-o", tmp]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode:
+        raise RuntimeError(f"linking failed:\n{' '.join(cmd)}\n{r.stdout}{r.stderr}")
+    os.replace(tmp, LIB)
+    if verbose:
+        print(f"built {LIB}")
+    return LIB
+
+
+if __name__ == "__main__":
+    try:
+        build()
+    except Exception as e:  # noqa: BLE001
+        print(e, file=sys.stderr)
+        sys.exit(1)

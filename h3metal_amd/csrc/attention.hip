@@ -1,0 +1,543 @@
+// Flash attention for gfx950 (CDNA4): out = softmax(scale * Q K^T) V per head,
+// with int8 or 16-bit scores and 16-bit P V, online softmax in fp32.
+//
+// Semantics follow the reference kernel kernels/attention.metal:70-394:
+//   Q [H][q_rows][D], K and V [KVH][k_rows][D], query head h reads key/value
+//   head h / (H / KVH) (:87); keys >= L are masked, and with causal masking
+//   query row i sees keys 0 .. i + causal_off (:115-117, :234-254); head h
+//   writes rows (h / seq_heads) * seq_rows + i, columns (h % seq_heads) * D of
+//   O (:384-385). With int8 scores (QK8) the score is
+//   (q_i . k_j) * qs_i * ks_j * scale in log2 units (:101-106, :209-217), the
+//   query scale applied in the exponent and the running maximum updated
+//   lazily, only when a score exceeds it by SLACK = 8 (:255-298); P is rounded
+//   to the value type before P V (:329-355); O is divided by the row sum at
+//   the end (:376-393).
+//
+// The gfx950 design (not the Metal one):
+//  * One workgroup = NW waves of 64 lanes; each wave owns 32 query rows of one
+//    head and the workgroup walks the keys in blocks of BK = 64, staged in LDS
+//    (double-buffered: the next block's global loads are in flight during this
+//    block's math). The 1-D grid is remapped so that each XCD (own L2) runs a
+//    contiguous range of (head, query-block) tiles: the tiles of one head share
+//    its K/V stream in that XCD's L2.
+//  * Scores are computed transposed, S^T = K Q^T, on the 32x32 MFMA
+//    (v_mfma_i32_32x32x32_i8 or v_mfma_f32_32x32x16_{bf16,f16}): an accumulator
+//    lane then holds 16 keys of ONE query (column = lane % 32), so the softmax
+//    state (max, sum, rescale) is per lane and only the partner lane (lane ^ 32,
+//    same query, other keys) ever has to be consulted.
+//  * The K rows of a 32-key tile are fed to the MFMA in the order
+//    pi(a) = 16*(a/16) + 8*((a/4)%2) + 4*((a/8)%2) + a%4, so that accumulator
+//    element i of lane-half h holds key 16*(i/8) + 8*h + i%8: each half of the
+//    accumulator is then, as it stands, the B operand (8 consecutive keys per
+//    lane) of one 32x32x16 P V MFMA computing O^T = V^T P^T. O^T lands with the
+//    same lane = query layout, so rescaling O is a per-lane multiply.
+//  * V is stored transposed in LDS (V^T[d][key], 16-byte pieces XOR-swizzled by
+//    d % 8) so that each P V operand is one 16-byte LDS read; K rows are
+//    swizzled by key bits so that the permuted row reads are bank-conflict free.
+#include "h3hip_internal.h"
+
+#include <cfloat>
+#include <cstring>
+#include <type_traits>
+#include <cmath>
+
+namespace h3 {
+namespace {
+
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+typedef int i32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
+typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+
+enum { T_I8 = 0, T_BF16 = 1, T_F16 = 2, T_F32 = 3 };
+
+constexpr int BK = 64;         // keys per LDS block
+constexpr float SLACK = 8.0f;  // log2 units the running maximum may lag behind a score
+
+template <int T> struct Vec8;
+template <> struct Vec8<T_BF16> { using type = bf16x8; using elem = __bf16; };
+template <> struct Vec8<T_F16> { using type = f16x8; using elem = _Float16; };
+
+// 32x32 product with a 16-byte A and B operand per lane.
+template <int QKT>
+__device__ __forceinline__ auto mma_qk(i32x4 a, i32x4 b, typename std::conditional<QKT == T_I8, i32x16, f32x16>::type c) {
+  if constexpr (QKT == T_I8) {
+    return __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b, c, 0, 0, 0);
+  } else if constexpr (QKT == T_BF16) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c,
+                                                   0, 0, 0);
+  } else {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c, 0,
+                                                  0, 0);
+  }
+}
+
+template <int VT>
+__device__ __forceinline__ f32x16 mma_pv(typename Vec8<VT>::type a, typename Vec8<VT>::type b, f32x16 c) {
+  if constexpr (VT == T_BF16) return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+  else return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+}
+
+// Swizzle of the 16-byte pieces of a K row in LDS: distinct for the 8 lanes
+// that read one LDS pass (keys differing in bits 0, 1 and 3).
+template <int NP>
+__device__ __forceinline__ int kswz(int key) {
+  return ((key & 3) | ((key >> 1) & 4)) & (NP - 1);
+}
+
+template <int OT>
+__device__ __forceinline__ void store4(char *dst, float a, float b, float c, float d) {
+  if constexpr (OT == T_F32) {
+    *(f32x4 *)dst = f32x4{a, b, c, d};
+  } else if constexpr (OT == T_BF16) {
+    typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+    *(bf16x4 *)dst = bf16x4{(__bf16)a, (__bf16)b, (__bf16)c, (__bf16)d};
+  } else {
+    typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+    *(f16x4 *)dst = f16x4{(_Float16)a, (_Float16)b, (_Float16)c, (_Float16)d};
+  }
+}
+
+template <int D, int QKT, int VT, int NW>
+struct Cfg {
+  static constexpr bool QK8 = QKT == T_I8;
+  static constexpr int NT = NW * 64;         // threads
+  static constexpr int BQ = NW * 32;         // query rows per workgroup
+  static constexpr int ESZ = QK8 ? 1 : 2;    // bytes per Q/K element
+  static constexpr int RB = D * ESZ;         // bytes per Q/K row
+  static constexpr int NP = RB / 16;         // 16-byte pieces per Q/K row
+  static constexpr int NCH = NP / 2;         // score MFMAs per 32x32 tile (one piece per lane half each)
+  static constexpr int KBYTES = BK * RB;
+  static constexpr int VBYTES = D * BK * 2;
+  static constexpr int SBYTES = QK8 ? BK * 4 : 0;
+  static constexpr int BUF = KBYTES + VBYTES + SBYTES;
+  static constexpr int LDS = 2 * BUF;
+  static constexpr int KPT = (BK * NP + NT - 1) / NT;   // K pieces staged per thread
+  static constexpr int NVT = (BK / 4) * (D / 8);        // V tasks: 4 keys x 8 channels
+  static constexpr int VPT = (NVT + NT - 1) / NT;
+  static_assert(D % 32 == 0 && D <= 128, "head dim");
+};
+
+// DUMP: instead of attention, write the raw score accumulators S[h][q][key]
+// (int32 for int8 inputs, fp32 otherwise) of the same MFMA path, for tests.
+template <int D, int QKT, int VT, int OT, bool CAUSAL, int NW, bool DUMP>
+__global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2, 2)))
+void attention_kernel(const char *__restrict__ Q, const char *__restrict__ K, const char *__restrict__ V,
+                      char *__restrict__ O, const float *__restrict__ qs, const float *__restrict__ ks, AttnParams p,
+                      int nqb) {
+  using C = Cfg<D, QKT, VT, NW>;
+  using VT8 = typename Vec8<VT>::type;
+  using VE = typename Vec8<VT>::elem;
+  using SAcc = typename std::conditional<C::QK8, i32x16, f32x16>::type;
+  extern __shared__ __attribute__((aligned(16))) char smem[];
+
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, hl = lane >> 5, l32 = lane & 31;
+  // XCD-aware tile order: workgroup b runs on XCD b % 8; give each XCD a contiguous range.
+  const int nb = gridDim.x, b = blockIdx.x;
+  const int per = nb >> 3, rem = nb & 7, xcd = b & 7, loc = b >> 3;
+  const int lid = (xcd < rem ? xcd * (per + 1) : rem * (per + 1) + (xcd - rem) * per) + loc;
+  const int h = lid / nqb, qb = lid - h * nqb;
+  const int kvh = h / (p.H / p.KVH);
+  const int q = qb * C::BQ + w * 32 + l32;  // this lane's query row
+  const bool qvalid = q < p.Lq;
+
+  // Q operand (B of S^T = K Q^T): row q, piece 2c + hl of each 32-byte chunk c.
+  i32x4 qreg[C::NCH];
+  {
+    const char *qrow = Q + ((size_t)h * p.q_rows + (qvalid ? q : 0)) * C::RB;
+#pragma unroll
+    for (int c = 0; c < C::NCH; c++)
+      qreg[c] = qvalid ? *(const i32x4 *)(qrow + (2 * c + hl) * 16) : i32x4{0, 0, 0, 0};
+  }
+  float qsc = p.scale;
+  if constexpr (C::QK8) qsc = qvalid ? fmaxf(qs[(size_t)h * p.q_rows + q] * p.scale, FLT_MIN) : 1.0f;
+
+  const char *Kh = K + (size_t)kvh * p.k_rows * C::RB;
+  const char *Vh = V + (size_t)kvh * p.k_rows * D * 2;
+  const float *ksh = C::QK8 ? ks + (size_t)kvh * p.k_rows : nullptr;
+  int kend = p.L;
+  if constexpr (CAUSAL) kend = min(p.L, qb * C::BQ + C::BQ + p.causal_off);
+
+  // staging registers for one key block
+  i32x4 kr[C::KPT];
+  u32x4 vr[C::VPT][4];
+  float ksr = 0.0f;
+  auto gload = [&](int kb) {
+#pragma unroll
+    for (int i = 0; i < C::KPT; i++) {
+      const int idx = tid + i * C::NT;
+      const int key = idx / C::NP, pc = idx % C::NP;
+      const bool ok = idx < BK * C::NP && kb + key < p.L;
+      kr[i] = ok ? *(const i32x4 *)(Kh + (size_t)(kb + key) * C::RB + pc * 16) : i32x4{0, 0, 0, 0};
+    }
+#pragma unroll
+    for (int i = 0; i < C::VPT; i++) {
+      const int task = tid + i * C::NT;
+      const int kg = task % (BK / 4), dg = task / (BK / 4);
+#pragma unroll
+      for (int r = 0; r < 4; r++) {
+        const int key = kb + 4 * kg + r;
+        const bool ok = task < C::NVT && key < p.L;
+        vr[i][r] = ok ? *(const u32x4 *)(Vh + (size_t)key * D * 2 + dg * 16) : u32x4{0, 0, 0, 0};
+      }
+    }
+    if constexpr (C::QK8) ksr = (tid < BK && kb + tid < p.L) ? ksh[kb + tid] : 0.0f;
+  };
+  auto lstore = [&](char *buf) {
+#pragma unroll
+    for (int i = 0; i < C::KPT; i++) {
+      const int idx = tid + i * C::NT;
+      const int key = idx / C::NP, pc = idx % C::NP;
+      if (idx < BK * C::NP) *(i32x4 *)(buf + key * C::RB + ((pc ^ kswz<C::NP>(key)) * 16)) = kr[i];
+    }
+    char *vt = buf + C::KBYTES;
+#pragma unroll
+    for (int i = 0; i < C::VPT; i++) {
+      const int task = tid + i * C::NT;
+      if (task < C::NVT) {
+        const int kg = task % (BK / 4), dg = task / (BK / 4);
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+          const int d = dg * 8 + j, sh = (j & 1) * 16;
+          const unsigned e0 = (vr[i][0][j >> 1] >> sh) & 0xffffu, e1 = (vr[i][1][j >> 1] >> sh) & 0xffffu;
+          const unsigned e2 = (vr[i][2][j >> 1] >> sh) & 0xffffu, e3 = (vr[i][3][j >> 1] >> sh) & 0xffffu;
+          *(u32x2 *)(vt + d * (BK * 2) + (((kg >> 1) ^ (d & 7)) * 16) + (kg & 1) * 8) =
+              u32x2{e0 | (e1 << 16), e2 | (e3 << 16)};
+        }
+      }
+    }
+    if constexpr (C::QK8) {
+      if (tid < BK) ((float *)(vt + C::VBYTES))[tid] = ksr;
+    }
+  };
+
+  f32x16 o[D / 32];
+#pragma unroll
+  for (int db = 0; db < D / 32; db++)
+#pragma unroll
+    for (int i = 0; i < 16; i++) o[db][i] = 0.0f;
+  float m = -INFINITY, l = 0.0f;
+
+  // K row this lane feeds to the score MFMA of a 32-key tile (before the tile offset)
+  const int krow = 16 * (l32 >> 4) + 8 * ((l32 >> 2) & 1) + 4 * ((l32 >> 3) & 1) + (l32 & 3);
+
+  if (kend > 0) {
+    gload(0);
+    lstore(smem);
+  }
+  __syncthreads();
+  int cur = 0;
+  for (int kb = 0; kb < kend; kb += BK) {
+    const bool more = kb + BK < kend;
+    if (more) gload(kb + BK);
+    const char *Ks = smem + cur * C::BUF;
+    const char *Vt = Ks + C::KBYTES;
+    const float *ksc = (const float *)(Vt + C::VBYTES);
+
+    // S^T tiles for keys kb + 32 t + (0..31)
+    SAcc s[2];
+#pragma unroll
+    for (int t = 0; t < 2; t++) {
+#pragma unroll
+      for (int i = 0; i < 16; i++) s[t][i] = 0;
+      const int key = 32 * t + krow;
+      const char *kp = Ks + key * C::RB;
+      const int sw = kswz<C::NP>(key);
+#pragma unroll
+      for (int c = 0; c < C::NCH; c++) {
+        const i32x4 a = *(const i32x4 *)(kp + (((2 * c + hl) ^ sw) * 16));
+        s[t] = mma_qk<QKT>(a, qreg[c], s[t]);
+      }
+    }
+
+    if constexpr (DUMP) {
+      // element i of lane-half hl holds key kb + 32 t + 16 (i / 8) + 8 hl + i % 8
+      if (qvalid) {
+#pragma unroll
+        for (int t = 0; t < 2; t++)
+#pragma unroll
+          for (int i = 0; i < 16; i++) {
+            const int key = kb + 32 * t + 16 * (i >> 3) + 8 * hl + (i & 7);
+            if (key < p.L) {
+              float *dst = (float *)O + ((size_t)h * p.Lq + q) * p.L + key;
+              if constexpr (C::QK8) *(int *)dst = s[t][i];
+              else *dst = s[t][i];
+            }
+          }
+      }
+    } else {
+      float x[2][16];
+#pragma unroll
+      for (int t = 0; t < 2; t++) {
+        if constexpr (C::QK8) {
+#pragma unroll
+          for (int s8 = 0; s8 < 2; s8++) {
+            const f32x4 k0 = *(const f32x4 *)(ksc + 32 * t + 16 * s8 + 8 * hl);
+            const f32x4 k1 = *(const f32x4 *)(ksc + 32 * t + 16 * s8 + 8 * hl + 4);
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+              x[t][8 * s8 + j] = (float)s[t][8 * s8 + j] * k0[j];
+              x[t][8 * s8 + 4 + j] = (float)s[t][8 * s8 + 4 + j] * k1[j];
+            }
+          }
+        } else {
+#pragma unroll
+          for (int i = 0; i < 16; i++) x[t][i] = s[t][i];
+        }
+      }
+      if (CAUSAL || kb + BK > p.L) {
+#pragma unroll
+        for (int t = 0; t < 2; t++)
+#pragma unroll
+          for (int i = 0; i < 16; i++) {
+            const int key = kb + 32 * t + 16 * (i >> 3) + 8 * hl + (i & 7);
+            bool masked = key >= p.L;
+            if constexpr (CAUSAL) masked = masked || key > q + p.causal_off;
+            if (masked) x[t][i] = -INFINITY;
+          }
+      }
+      float amax = -INFINITY;
+#pragma unroll
+      for (int t = 0; t < 2; t++)
+#pragma unroll
+        for (int i = 0; i < 16; i++) amax = fmaxf(amax, x[t][i]);
+      // lazy running maximum (wave-uniform branch); partner lanes always update together
+      if (__any(amax * qsc > m + SLACK)) {
+        const float ap = fmaxf(amax, __shfl_xor(amax, 32));
+        const float mn = fmaxf(m, ap * qsc);
+        const float f = mn == -INFINITY ? 1.0f : __builtin_amdgcn_exp2f(m - mn);
+        m = mn;
+        l *= f;
+#pragma unroll
+        for (int db = 0; db < D / 32; db++)
+#pragma unroll
+          for (int i = 0; i < 16; i++) o[db][i] *= f;
+      }
+      const float nm = m == -INFINITY ? 0.0f : -m;
+      VT8 pb[2][2];
+#pragma unroll
+      for (int t = 0; t < 2; t++)
+#pragma unroll
+        for (int i = 0; i < 16; i++) {
+          const float pv = __builtin_amdgcn_exp2f(fmaf(x[t][i], qsc, nm));
+          l += pv;
+          pb[t][i >> 3][i & 7] = (VE)pv;
+        }
+      // O^T += V^T P^T, 16 keys per MFMA
+#pragma unroll
+      for (int t = 0; t < 2; t++)
+#pragma unroll
+        for (int s2 = 0; s2 < 2; s2++) {
+          const int kp = 4 * t + 2 * s2 + hl;
+#pragma unroll
+          for (int db = 0; db < D / 32; db++) {
+            const int d = db * 32 + l32;
+            const VT8 a = *(const VT8 *)(Vt + d * (BK * 2) + ((kp ^ (d & 7)) * 16));
+            o[db] = mma_pv<VT>(a, pb[t][s2], o[db]);
+          }
+        }
+    }
+    if (more) lstore(smem + (cur ^ 1) * C::BUF);
+    __syncthreads();
+    cur ^= 1;
+  }
+  if constexpr (!DUMP) {
+    const float lt = l + __shfl_xor(l, 32);
+    const float inv = lt > 0.0f ? 1.0f / lt : 0.0f;
+    if (qvalid) {
+      constexpr int OSZ = OT == T_F32 ? 4 : 2;
+      const int seq = h / p.seq_heads;
+      char *orow = O + (((size_t)seq * p.seq_rows + q) * p.o_stride + (size_t)(h - seq * p.seq_heads) * D) * OSZ;
+#pragma unroll
+      for (int db = 0; db < D / 32; db++)
+#pragma unroll
+        for (int g = 0; g < 4; g++) {
+          const int d = db * 32 + 8 * g + 4 * hl;
+          store4<OT>(orow + d * OSZ, o[db][4 * g] * inv, o[db][4 * g + 1] * inv, o[db][4 * g + 2] * inv,
+                     o[db][4 * g + 3] * inv);
+        }
+    }
+  }
+}
+
+constexpr int NW_DEFAULT = 4;
+
+int esize(int t) { return t == T_I8 ? 1 : t == T_F32 ? 4 : 2; }
+
+// Host side: validation (every access the kernel makes must fall inside the
+// bound buffers) and launch.
+template <int D, int QKT, int VT, int OT, bool CAUSAL, bool DUMP>
+int launch_attention(const Pipeline &pl, hipStream_t stream, const Arg *args, int nargs, const void *params,
+                     uint32_t params_len, std::string *err) {
+  constexpr int NW = NW_DEFAULT;
+  using C = Cfg<D, QKT, VT, NW>;
+  if (params_len != sizeof(AttnParams)) {
+    *err = "parameter block of " + std::to_string(params_len) + " bytes, expected " +
+           std::to_string(sizeof(AttnParams));
+    return -1;
+  }
+  AttnParams p;
+  memcpy(&p, params, sizeof p);
+  if (p.Lq < 0 || p.L < 1 || p.H < 1 || p.KVH < 1 || p.H % p.KVH || p.q_rows < p.Lq || p.k_rows < p.L ||
+      p.o_stride < 0) {
+    *err = "bad shape: Lq " + std::to_string(p.Lq) + " L " + std::to_string(p.L) + " H " + std::to_string(p.H) +
+           " KVH " + std::to_string(p.KVH) + " q_rows " + std::to_string(p.q_rows) + " k_rows " +
+           std::to_string(p.k_rows);
+    return -1;
+  }
+  if (p.seq_heads < 1) p.seq_heads = p.H;
+  if (!(p.scale > 0.0f) || !std::isfinite(p.scale)) {
+    *err = "softmax scale must be positive and finite";
+    return -1;
+  }
+  const bool qk8 = C::QK8;
+  const int need = qk8 ? 7 : 4;
+  if (nargs < need) {
+    *err = "expected buffers q, k, v, out" + std::string(qk8 ? ", -, q_scale, k_scale" : "");
+    return -1;
+  }
+  for (int i : {0, 1, 2, 3})
+    if (!args[i].ptr) {
+      *err = "buffer " + std::to_string(i) + " (q, k, v, out) is not bound";
+      return -1;
+    }
+  if (qk8 && (!args[5].ptr || !args[6].ptr)) {
+    *err = "int8 scores need q_scale and k_scale";
+    return -1;
+  }
+  auto fits = [&](int i, uint64_t bytes, const char *what) {
+    if (bytes > args[i].avail) {
+      *err = std::string(what) + " needs " + std::to_string(bytes) + " bytes, its buffer holds " +
+             std::to_string(args[i].avail);
+      return false;
+    }
+    return true;
+  };
+  const uint64_t es = esize(QKT);
+  if (!fits(0, (uint64_t)p.H * p.q_rows * D * es, "q") || !fits(1, (uint64_t)p.KVH * p.k_rows * D * es, "k") ||
+      !fits(2, (uint64_t)p.KVH * p.k_rows * D * 2, "v"))
+    return -1;
+  if (qk8 && (!fits(5, (uint64_t)p.H * p.q_rows * 4, "q_scale") || !fits(6, (uint64_t)p.KVH * p.k_rows * 4, "k_scale")))
+    return -1;
+  if (DUMP) {
+    if (!fits(3, (uint64_t)p.H * p.Lq * p.L * 4, "scores")) return -1;
+  } else if (p.Lq > 0) {
+    uint64_t last = 0;
+    for (int h = 0; h < p.H; h++) {
+      const uint64_t seq = h / p.seq_heads;
+      const uint64_t end = ((seq * p.seq_rows + p.Lq - 1) * (uint64_t)p.o_stride + (uint64_t)(h % p.seq_heads) * D + D);
+      last = end > last ? end : last;
+    }
+    if ((uint64_t)p.o_stride < (uint64_t)p.seq_heads * D && p.H > 1 && p.seq_heads > 1) {
+      *err = "o_stride " + std::to_string(p.o_stride) + " smaller than seq_heads * D";
+      return -1;
+    }
+    if (!fits(3, last * esize(OT), "out")) return -1;
+  }
+  if (p.Lq == 0) return 0;
+  const int nqb = (p.Lq + C::BQ - 1) / C::BQ;
+  const long nblk = (long)nqb * p.H;
+  if (nblk > 0x7fffffffL) {
+    *err = "grid too large";
+    return -1;
+  }
+  auto kern = attention_kernel<D, QKT, VT, OT, CAUSAL, NW, DUMP>;
+  static bool attr_set = false;
+  if (!attr_set) {
+    hipError_t e = hipFuncSetAttribute((const void *)kern, hipFuncAttributeMaxDynamicSharedMemorySize, C::LDS);
+    if (e != hipSuccess) {
+      *err = std::string("hipFuncSetAttribute: ") + hipGetErrorString(e);
+      return -1;
+    }
+    attr_set = true;
+  }
+  hipLaunchKernelGGL(kern, dim3((unsigned)nblk), dim3(C::NT), C::LDS, stream, args[0].ptr, args[1].ptr, args[2].ptr,
+                     args[3].ptr, (const float *)args[5].ptr, (const float *)args[6].ptr, p, nqb);
+  (void)pl;
+  return 0;
+}
+
+template <int D, int QKT, int VT, int OT, bool DUMP>
+LaunchFn pick_causal(bool causal) {
+  if (DUMP) return launch_attention<D, QKT, VT, OT, false, DUMP>;
+  return causal ? launch_attention<D, QKT, VT, OT, true, DUMP> : launch_attention<D, QKT, VT, OT, false, DUMP>;
+}
+
+template <int D, int QKT, int VT, bool DUMP>
+LaunchFn pick_out(int ot, bool causal) {
+  if (DUMP) return pick_causal<D, QKT, VT, T_F32, true>(false);
+  switch (ot) {
+    case T_BF16: return pick_causal<D, QKT, VT, T_BF16, false>(causal);
+    case T_F16: return pick_causal<D, QKT, VT, T_F16, false>(causal);
+    default: return pick_causal<D, QKT, VT, T_F32, false>(causal);
+  }
+}
+
+template <int D, bool DUMP>
+LaunchFn pick_types(int qkt, int vt, int ot, bool causal) {
+  if (qkt == T_I8) {
+    return vt == T_BF16 ? pick_out<D, T_I8, T_BF16, DUMP>(ot, causal) : pick_out<D, T_I8, T_F16, DUMP>(ot, causal);
+  }
+  return qkt == T_BF16 ? pick_out<D, T_BF16, T_BF16, DUMP>(ot, causal) : pick_out<D, T_F16, T_F16, DUMP>(ot, causal);
+}
+
+int type_of(const std::string &s) {
+  if (s == "bfloat" || s == "bf16") return T_BF16;
+  if (s == "half" || s == "f16") return T_F16;
+  if (s == "float" || s == "f32") return T_F32;
+  return -1;
+}
+
+}  // namespace
+
+// Specialisation macros: HD (head dim: 64 or 128), QK8 (int8 scores), O_T
+// (output: half | bfloat | float), CAUSAL, and IN_T (half | bfloat: the type of
+// V, and of Q and K without QK8; the reference's inputs are half). The
+// reference's tuning macros WM, BK, KPAD, DB, PVORDER, VX, SLACK are accepted
+// as integers and do not change the gfx950 kernel (its tiles are its own).
+bool make_attention(const std::string &fn, const Macros &m, Pipeline *pl, std::string *err) {
+  const bool dump = fn == "attention_scores";
+  if (fn != "attention" && !dump) {
+    *err = "unknown function (have: attention, attention_scores)";
+    return false;
+  }
+  int hd, qk8, causal, dummy;
+  if (!macro_int(m, "HD", 128, &hd, err) || !macro_int(m, "QK8", 0, &qk8, err) ||
+      !macro_int(m, "CAUSAL", 0, &causal, err))
+    return false;
+  for (const char *k : {"WM", "BK", "KPAD", "DB", "PVORDER", "VX", "SLACK", "TG"})
+    if (!macro_int(m, k, 0, &dummy, err)) return false;
+  for (auto &kv : m) {
+    static const char *known[] = {"HD", "QK8", "CAUSAL", "O_T", "IN_T", "WM", "BK", "KPAD", "DB", "PVORDER", "VX",
+                                  "SLACK", "TG"};
+    bool ok = false;
+    for (const char *k : known) ok = ok || kv.first == k;
+    if (!ok) {
+      *err = "unknown macro " + kv.first;
+      return false;
+    }
+  }
+  const int ot = type_of(macro_str(m, "O_T", "half"));
+  const int it = type_of(macro_str(m, "IN_T", "half"));
+  if (ot < 0 || it < 0 || it == T_F32) {
+    *err = "O_T must be half|bfloat|float and IN_T half|bfloat";
+    return false;
+  }
+  if (hd != 64 && hd != 128) {
+    *err = "HD " + std::to_string(hd) + " not supported (64 or 128)";
+    return false;
+  }
+  const int qkt = qk8 ? T_I8 : it;
+  LaunchFn f;
+  if (hd == 128) f = dump ? pick_types<128, true>(qkt, it, ot, causal) : pick_types<128, false>(qkt, it, ot, causal);
+  else f = dump ? pick_types<64, true>(qkt, it, ot, causal) : pick_types<64, false>(qkt, it, ot, causal);
+  pl->launch = f;
+  pl->threads = NW_DEFAULT * 64;
+  return true;
+}
+
+}  // namespace h3

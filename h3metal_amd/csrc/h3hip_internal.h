@@ -1,0 +1,68 @@
+// Internal declarations shared by the runtime (capi.hip) and the kernel modules.
+//
+// Parameter blocks keep the reference's byte layout, because the Python launchers
+// pack them with struct exactly as the reference does:
+//   AttnParams   <- kernels/params.h:41-53, packed by h3metal/ops.py:187-188 ("7if3i")
+//   QkRopeParams <- kernels/ops.metal:344-349, packed by h3metal/ops.py:237 ("8ifi")
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <map>
+#include <string>
+
+namespace h3 {
+
+struct AttnParams {
+  int Lq;          // query rows
+  int L;           // keys (keys >= L are masked)
+  int H;           // query heads
+  int KVH;         // key/value heads (query head h reads key/value head h / (H / KVH))
+  int q_rows;      // rows reserved per head in Q (and in the query scales)
+  int k_rows;      // rows reserved per key/value head in K, V (and in the key scales)
+  int o_stride;    // elements between rows of the output
+  float scale;     // softmax scale times log2(e)
+  int causal_off;  // with causal masking: query row i sees keys 0 .. i + causal_off
+  int seq_heads;   // heads per sequence: head h writes rows of sequence h / seq_heads
+  int seq_rows;    // output rows between consecutive sequences
+};
+static_assert(sizeof(AttnParams) == 44, "AttnParams must match struct.pack('<7if3i')");
+
+struct QkRopeParams {
+  int M, Hq, Hk, Hv, in_stride, out_rows, rot, norm;
+  float eps;
+  int seq_len;  // rows per sequence: row m is row m % seq_len of sequence m / seq_len
+};
+static_assert(sizeof(QkRopeParams) == 40, "QkRopeParams must match struct.pack('<8ifi')");
+
+using Macros = std::map<std::string, std::string>;
+
+// One bound buffer argument as the launchers see it: a device address and the
+// bytes available from it to the end of its buffer (0 / nullptr when unbound).
+struct Arg {
+  char *ptr = nullptr;
+  uint64_t avail = 0;
+};
+
+struct Pipeline;
+using LaunchFn = int (*)(const Pipeline &pl, hipStream_t stream, const Arg *args, int nargs, const void *params,
+                         uint32_t params_len, std::string *err);
+
+// A selected kernel specialisation (what h3_pipeline returns).
+struct Pipeline {
+  std::string name;   // "module:fn(macros)" for messages
+  LaunchFn launch = nullptr;
+  int threads = 0;    // threads per workgroup of the launch
+  int ival[8] = {};   // module-specific specialisation values
+};
+
+// Module factories: fill `pl` for (fn, macros) or return false with a message.
+bool make_attention(const std::string &fn, const Macros &m, Pipeline *pl, std::string *err);
+bool make_ops(const std::string &fn, const Macros &m, Pipeline *pl, std::string *err);
+
+// Helpers for macro parsing in the factories.
+bool macro_int(const Macros &m, const char *key, int def, int *out, std::string *err);
+std::string macro_str(const Macros &m, const char *key, const char *def);
+
+}  // namespace h3

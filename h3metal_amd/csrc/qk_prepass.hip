@@ -1,0 +1,320 @@
+// Queries/keys pre-pass for attention, fused in one kernel for gfx950:
+// per-head RMS norm, rotary embedding, Walsh-Hadamard rotation with fixed
+// signs, and per-row int8 quantisation; values are copied through.
+//
+// Semantics of the reference kernel qk_norm_rope (kernels/ops.metal:365-468,
+// parameters :344-349, launcher h3metal/ops.py:225-239):
+//  * Input rows hold Hq query heads, then Hk key heads, then Hv value heads of
+//    HDIM channels each (a "slot" is one of them); row m is row r = m % seq_len
+//    of sequence m / seq_len, whose heads are output heads sq*H .. sq*H + H-1,
+//    row r of each (:381, :448).
+//  * norm: v = (v * 1/sqrt(sum(v^2)/HDIM + eps)) * w (:394-402).
+//  * rot: the first `rot` channels are rotated in pairs (i, i + rot/2) by the
+//    row's angle table: v_i c - v_{i+rot/2} s and v_{i+rot/2} c + v_i s (:403-419).
+//  * QKROT (int8 outputs only): v_c = -v_c where popcount(c * 0x2545F491) is odd,
+//    then a 128-point fast Walsh-Hadamard transform with its butterfly stages in
+//    increasing channel-bit order, each (a + b, a - b) with a the lower channel,
+//    then a multiply by 1/sqrt(HDIM) (:420-446).
+//  * QK8: scale = amax > 0 ? amax / 127 : 1, code = rint(v / scale) (:450-458).
+// Every floating-point step is a single IEEE-rounded operation in that order
+// (this file is compiled without FMA contraction; division and square root are
+// correctly rounded), so a float32 restatement reproduces codes and scales bit
+// for bit. The sum of squares is summed per lane, then over the 32 lanes of a
+// head with an xor butterfly (strides 16, 8, 4, 2, 1): a fixed order.
+//
+// gfx950 layout: a wave of 64 lanes handles two slots, 32 lanes per slot and
+// HDIM/32 channels per lane (lane l: channels l*PER .. l*PER + PER-1), so every
+// cross-lane step stays inside a half wave; a workgroup of 256 threads handles
+// 8 slots of one row. The kernel is HBM-bound: one read of the row, one write
+// of the codes / halves.
+#include "h3hip_internal.h"
+
+#include <cmath>
+#include <cstring>
+
+namespace h3 {
+namespace {
+
+enum { T_I8 = 0, T_BF16 = 1, T_F16 = 2, T_F32 = 3 };
+
+template <int T> struct Elem;
+template <> struct Elem<T_BF16> { using type = __bf16; };
+template <> struct Elem<T_F16> { using type = _Float16; };
+template <> struct Elem<T_F32> { using type = float; };
+
+template <int N, typename E> struct VecOf { typedef E type __attribute__((ext_vector_type(N))); };
+
+constexpr int SLOTS_PER_WG = 8;
+
+template <int HDIM>
+constexpr double inv_sqrt_hdim() {
+  return HDIM == 128 ? 0.0883883476483184405501055452631 : HDIM == 64 ? 0.125 : 0.1767766952966368811;
+}
+
+template <int HDIM, int IN_T, int QK_T, int V_T, bool QKROT>
+__global__ __launch_bounds__(256) void qk_norm_rope_kernel(const char *__restrict__ in, const float *__restrict__ wq,
+                                                            const float *__restrict__ wk,
+                                                            const float *__restrict__ cs,
+                                                            const float *__restrict__ sn, char *__restrict__ Qo,
+                                                            char *__restrict__ Ko, char *__restrict__ Vo,
+                                                            float *__restrict__ qsc, float *__restrict__ ksc,
+                                                            QkRopeParams p) {
+  constexpr int PER = HDIM / 32;
+  using IE = typename Elem<IN_T>::type;
+  const int lane = threadIdx.x & 63, hl = lane >> 5, l32 = lane & 31, w = threadIdx.x >> 6;
+  const int m = blockIdx.x;
+  const int sq = m / p.seq_len, r = m - sq * p.seq_len;
+  const int slot = blockIdx.y * SLOTS_PER_WG + w * 2 + hl;
+  const int nslots = p.Hq + p.Hk + p.Hv;
+  if (slot >= nslots) return;  // whole half-waves only; no cross-lane step crosses halves
+
+  float v[PER];
+  {
+    const IE *src = (const IE *)in + (size_t)m * p.in_stride + (size_t)slot * HDIM + l32 * PER;
+    typedef typename VecOf<PER, IE>::type IV;
+    const IV x = *(const IV *)src;
+#pragma unroll
+    for (int i = 0; i < PER; i++) v[i] = (float)x[i];
+  }
+
+  if (slot < p.Hq + p.Hk) {
+    const bool isq = slot < p.Hq;
+    const int h = isq ? slot : slot - p.Hq;
+    if (p.norm) {
+      float ss = v[0] * v[0];
+#pragma unroll
+      for (int i = 1; i < PER; i++) ss = ss + v[i] * v[i];
+#pragma unroll
+      for (int s = 16; s >= 1; s >>= 1) ss = ss + __shfl_xor(ss, s);
+      const float inv = 1.0f / sqrtf(ss / (float)HDIM + p.eps);
+      const float *wv = (isq ? wq : wk) + l32 * PER;
+#pragma unroll
+      for (int i = 0; i < PER; i++) v[i] = (v[i] * inv) * wv[i];
+    }
+    if (p.rot) {
+      const int half_rot = p.rot / 2;
+      const int lanes = half_rot / PER;  // lanes holding the first half of the rotated channels
+      const int src_lane = l32 < lanes ? l32 + lanes : (l32 < 2 * lanes ? l32 - lanes : l32);
+      float pv[PER];
+#pragma unroll
+      for (int i = 0; i < PER; i++) pv[i] = __shfl(v[i], (lane & 32) + src_lane);
+      if (l32 < 2 * lanes) {
+        const bool first = l32 < lanes;
+        const int base = (first ? l32 : l32 - lanes) * PER;  // pair index of v[0]
+        const float *c = cs + (size_t)r * half_rot + base;
+        const float *s = sn + (size_t)r * half_rot + base;
+#pragma unroll
+        for (int i = 0; i < PER; i++) v[i] = first ? v[i] * c[i] - pv[i] * s[i] : v[i] * c[i] + pv[i] * s[i];
+      }
+    }
+    if constexpr (QKROT) {
+#pragma unroll
+      for (int i = 0; i < PER; i++) {
+        const unsigned c = (unsigned)(l32 * PER + i);
+        if (__builtin_popcount(c * 0x2545F491u) & 1u) v[i] = -v[i];
+      }
+#pragma unroll
+      for (int s = 1; s < PER; s <<= 1) {
+#pragma unroll
+        for (int i = 0; i < PER; i++) {
+          if (!(i & s)) {
+            const float a = v[i], b = v[i + s];
+            v[i] = a + b;
+            v[i + s] = a - b;
+          }
+        }
+      }
+#pragma unroll
+      for (int ls = 1; ls < 32; ls <<= 1) {
+#pragma unroll
+        for (int i = 0; i < PER; i++) {
+          const float o = __shfl_xor(v[i], ls);
+          v[i] = (l32 & ls) ? o - v[i] : v[i] + o;
+        }
+      }
+      constexpr float rn = (float)inv_sqrt_hdim<HDIM>();
+#pragma unroll
+      for (int i = 0; i < PER; i++) v[i] *= rn;
+    }
+    const size_t hrow = isq ? ((size_t)sq * p.Hq + h) * p.out_rows + r : ((size_t)sq * p.Hk + h) * p.out_rows + r;
+    if constexpr (QK_T == T_I8) {
+      float amax = 0.0f;
+#pragma unroll
+      for (int i = 0; i < PER; i++) amax = fmaxf(amax, fabsf(v[i]));
+#pragma unroll
+      for (int s = 16; s >= 1; s >>= 1) amax = fmaxf(amax, __shfl_xor(amax, s));
+      const float scale = amax > 0.0f ? amax / 127.0f : 1.0f;
+      typedef typename VecOf<PER, signed char>::type CV;
+      CV codes;
+#pragma unroll
+      for (int i = 0; i < PER; i++) codes[i] = (signed char)(int)rintf(v[i] / scale);
+      *(CV *)((isq ? Qo : Ko) + hrow * HDIM + l32 * PER) = codes;
+      if (l32 == 0) (isq ? qsc : ksc)[hrow] = scale;
+    } else {
+      using OE = typename Elem<QK_T>::type;
+      typedef typename VecOf<PER, OE>::type OV;
+      OV out;
+#pragma unroll
+      for (int i = 0; i < PER; i++) out[i] = (OE)v[i];
+      *(OV *)((isq ? Qo : Ko) + (hrow * HDIM + l32 * PER) * sizeof(OE)) = out;
+    }
+  } else {
+    using OE = typename Elem<V_T>::type;
+    typedef typename VecOf<PER, OE>::type OV;
+    OV out;
+#pragma unroll
+    for (int i = 0; i < PER; i++) out[i] = (OE)v[i];
+    const size_t vrow = ((size_t)sq * p.Hv + slot - p.Hq - p.Hk) * p.out_rows + r;
+    *(OV *)(Vo + (vrow * HDIM + l32 * PER) * sizeof(OE)) = out;
+  }
+}
+
+int esize(int t) { return t == T_I8 ? 1 : t == T_F32 ? 4 : 2; }
+
+template <int HDIM, int IN_T, int QK_T, int V_T, bool QKROT>
+int launch_qk(const Pipeline &pl, hipStream_t stream, const Arg *a, int nargs, const void *params,
+              uint32_t params_len, std::string *err) {
+  (void)pl;
+  if (params_len != sizeof(QkRopeParams)) {
+    *err = "parameter block of " + std::to_string(params_len) + " bytes, expected " +
+           std::to_string(sizeof(QkRopeParams));
+    return -1;
+  }
+  QkRopeParams p;
+  memcpy(&p, params, sizeof p);
+  const int PER = HDIM / 32;
+  const int nslots = p.Hq + p.Hk + p.Hv;
+  if (p.M < 0 || p.Hq < 0 || p.Hk < 0 || p.Hv < 0 || nslots < 1 || p.seq_len < 1 || p.out_rows < 1 ||
+      p.in_stride < nslots * HDIM) {
+    *err = "bad shape: M " + std::to_string(p.M) + " heads " + std::to_string(p.Hq) + "/" + std::to_string(p.Hk) +
+           "/" + std::to_string(p.Hv) + " in_stride " + std::to_string(p.in_stride) + " seq_len " +
+           std::to_string(p.seq_len);
+    return -1;
+  }
+  const int rows = p.M < p.seq_len ? p.M : p.seq_len;  // rows per sequence actually present
+  if (rows > p.out_rows) {
+    *err = "out_rows " + std::to_string(p.out_rows) + " smaller than the rows of a sequence";
+    return -1;
+  }
+  if (p.rot < 0 || p.rot > HDIM || p.rot % 2 || (p.rot / 2) % PER) {
+    *err = "rot " + std::to_string(p.rot) + " must be even, at most HD, and rot/2 a multiple of " +
+           std::to_string(PER);
+    return -1;
+  }
+  if (p.norm && !(p.eps >= 0.0f)) {
+    *err = "eps must be non-negative";
+    return -1;
+  }
+  if (nargs < 11 && QK_T == T_I8) {
+    *err = "int8 outputs need buffers q_scale and k_scale (indices 9, 10)";
+    return -1;
+  }
+  if (nargs < 8) {
+    *err = "expected buffers qkv, wq, wk, cos, sin, Q, K, V";
+    return -1;
+  }
+  auto need = [&](int i, uint64_t bytes, const char *what, bool required) {
+    if (!required || bytes == 0) return true;
+    if (!a[i].ptr) {
+      *err = std::string(what) + " is not bound";
+      return false;
+    }
+    if (bytes > a[i].avail) {
+      *err = std::string(what) + " needs " + std::to_string(bytes) + " bytes, its buffer holds " +
+             std::to_string(a[i].avail);
+      return false;
+    }
+    return true;
+  };
+  const uint64_t nseq = p.M ? (uint64_t)(p.M - 1) / p.seq_len + 1 : 0;
+  const uint64_t in_bytes = p.M ? ((uint64_t)(p.M - 1) * p.in_stride + (uint64_t)nslots * HDIM) * esize(IN_T) : 0;
+  const uint64_t hq = nseq * p.Hq * p.out_rows, hk = nseq * p.Hk * p.out_rows, hv = nseq * p.Hv * p.out_rows;
+  const uint64_t tab = (uint64_t)rows * (p.rot / 2) * 4;
+  if (!need(0, in_bytes, "qkv", true) || !need(1, HDIM * 4, "wq", p.norm && p.Hq) ||
+      !need(2, HDIM * 4, "wk", p.norm && p.Hk) || !need(3, tab, "cos", p.rot > 0 && (p.Hq + p.Hk)) ||
+      !need(4, tab, "sin", p.rot > 0 && (p.Hq + p.Hk)) || !need(5, hq * HDIM * esize(QK_T), "Q", p.Hq > 0) ||
+      !need(6, hk * HDIM * esize(QK_T), "K", p.Hk > 0) || !need(7, hv * HDIM * esize(V_T), "V", p.Hv > 0))
+    return -1;
+  if (QK_T == T_I8 && (!need(9, hq * 4, "q_scale", p.Hq > 0) || !need(10, hk * 4, "k_scale", p.Hk > 0))) return -1;
+  if (p.M == 0) return 0;
+  dim3 grid((unsigned)p.M, (unsigned)((nslots + SLOTS_PER_WG - 1) / SLOTS_PER_WG));
+  hipLaunchKernelGGL((qk_norm_rope_kernel<HDIM, IN_T, QK_T, V_T, QKROT>), grid, dim3(256), 0, stream, a[0].ptr,
+                     (const float *)a[1].ptr, (const float *)a[2].ptr, (const float *)a[3].ptr,
+                     (const float *)a[4].ptr, a[5].ptr, a[6].ptr, a[7].ptr, nargs > 9 ? (float *)a[9].ptr : nullptr,
+                     nargs > 10 ? (float *)a[10].ptr : nullptr, p);
+  return 0;
+}
+
+template <int HDIM, int IN_T>
+LaunchFn pick_out(int qk_t, int v_t, bool rot, std::string *err) {
+  if (qk_t == T_I8) {
+    if (v_t == T_BF16) return rot ? launch_qk<HDIM, IN_T, T_I8, T_BF16, true> : launch_qk<HDIM, IN_T, T_I8, T_BF16, false>;
+    return rot ? launch_qk<HDIM, IN_T, T_I8, T_F16, true> : launch_qk<HDIM, IN_T, T_I8, T_F16, false>;
+  }
+  if (rot) {
+    *err = "QKROT needs QK8 (int8 outputs)";
+    return nullptr;
+  }
+  if (qk_t == T_BF16)
+    return v_t == T_BF16 ? launch_qk<HDIM, IN_T, T_BF16, T_BF16, false> : launch_qk<HDIM, IN_T, T_BF16, T_F16, false>;
+  return v_t == T_BF16 ? launch_qk<HDIM, IN_T, T_F16, T_BF16, false> : launch_qk<HDIM, IN_T, T_F16, T_F16, false>;
+}
+
+template <int HDIM>
+LaunchFn pick_in(int in_t, int qk_t, int v_t, bool rot, std::string *err) {
+  switch (in_t) {
+    case T_BF16: return pick_out<HDIM, T_BF16>(qk_t, v_t, rot, err);
+    case T_F16: return pick_out<HDIM, T_F16>(qk_t, v_t, rot, err);
+    default: return pick_out<HDIM, T_F32>(qk_t, v_t, rot, err);
+  }
+}
+
+int type_of(const std::string &s) {
+  if (s == "bfloat" || s == "bf16") return T_BF16;
+  if (s == "half" || s == "f16") return T_F16;
+  if (s == "float" || s == "f32") return T_F32;
+  return -1;
+}
+
+}  // namespace
+
+// Specialisation macros: HDIM (64 or 128), IN_T (input: half | bfloat | float),
+// QK8 (int8 Q/K + scales), QKROT (rotation; needs QK8), QK_T (Q/K without QK8:
+// half | bfloat, default half as in the reference), V_T (half | bfloat, default
+// half). NSG (the reference's SIMD-groups per threadgroup) is accepted and unused.
+bool make_ops(const std::string &fn, const Macros &m, Pipeline *pl, std::string *err) {
+  if (fn != "qk_norm_rope") {
+    *err = "unknown function (have: qk_norm_rope)";
+    return false;
+  }
+  int hd, q8, rot, nsg;
+  if (!macro_int(m, "HDIM", 128, &hd, err) || !macro_int(m, "QK8", 0, &q8, err) ||
+      !macro_int(m, "QKROT", 0, &rot, err) || !macro_int(m, "NSG", 8, &nsg, err))
+    return false;
+  for (auto &kv : m) {
+    static const char *known[] = {"HDIM", "IN_T", "QK8", "QKROT", "QK_T", "V_T", "NSG"};
+    bool ok = false;
+    for (const char *k : known) ok = ok || kv.first == k;
+    if (!ok) {
+      *err = "unknown macro " + kv.first;
+      return false;
+    }
+  }
+  const int in_t = type_of(macro_str(m, "IN_T", "half"));
+  const int qk_t = q8 ? T_I8 : type_of(macro_str(m, "QK_T", "half"));
+  const int v_t = type_of(macro_str(m, "V_T", "half"));
+  if (in_t < 0 || qk_t < 0 || qk_t == T_F32 || v_t < 0 || v_t == T_F32) {
+    *err = "IN_T must be half|bfloat|float, QK_T and V_T half|bfloat";
+    return false;
+  }
+  LaunchFn f = nullptr;
+  if (hd == 128) f = pick_in<128>(in_t, qk_t, v_t, rot != 0, err);
+  else if (hd == 64) f = pick_in<64>(in_t, qk_t, v_t, rot != 0, err);
+  else *err = "HDIM " + std::to_string(hd) + " not supported (64 or 128)";
+  if (!f) return false;
+  pl->launch = f;
+  pl->threads = 256;
+  return true;
+}
+
+}  // namespace h3

@@ -1,0 +1,86 @@
+"""Launchers of the attention path: one Python function per GPU operation.
+
+Drop-in for the two launchers of the reference's h3metal/ops.py on the DiT
+attention path, with the same arguments, buffer layouts, parameter blocks and
+return value (None; results are valid after `gpu.wait()`):
+
+  attention     <- h3metal/ops.py:177-191
+  qk_norm_rope  <- h3metal/ops.py:225-239
+  pad_rows      <- h3metal/ops.py:116-117
+
+Element types come from the tensors, as in the reference (`OUT_DT`,
+ops.py:17). The gfx950 kernels additionally accept bf16 Q/K/V (the reference's
+attention inputs are half), passed to the kernel as the IN_T / QK_T / V_T
+specialisations.
+"""
+
+from __future__ import annotations
+
+from .gpu import Gpu, Tensor, pack
+
+OUT_DT = {"f16": "half", "bf16": "bfloat", "f32": "float"}
+LOG2E = 1.4426950408889634
+
+
+def pad_rows(m: int, tile: int = 128) -> int:
+    return (m + tile - 1) // tile * tile
+
+
+def attention(gpu: Gpu, q: Tensor, k: Tensor, v: Tensor, out: Tensor, *, Lq: int, L: int, H: int, KVH: int,
+              D: int, q_rows: int, k_rows: int, scale: float, causal: bool = False, causal_off: int = 0,
+              wm: int = 8, bk: int = 32, seq_heads: int | None = None, seq_rows: int = 0,
+              q_scale: Tensor | None = None, k_scale: Tensor | None = None, **variant):
+    """out = softmax(q k^T * scale) v per head (int8 scores when q_scale / k_scale are given).
+
+    q [H][q_rows][D], k and v [KVH][k_rows][D]; out rows (h // seq_heads) * seq_rows + i, columns
+    (h % seq_heads) * D, row stride seq_heads * D. wm, bk and the reference's variant flags (DB, PVORDER, VX, KPAD,
+    TG, SLACK) are tuning hints of the Metal kernel: accepted, and the gfx950 kernel uses its own tiles."""
+    variant.pop("TG", None)
+    q8 = q_scale is not None
+    if q8 != (k_scale is not None):
+        raise ValueError("attention: q_scale and k_scale go together")
+    if q8 and (q.dtype != "i8" or k.dtype != "i8"):
+        raise ValueError(f"attention: int8 scores need i8 q and k, got {q.dtype}, {k.dtype}")
+    if not q8 and (q.dtype != k.dtype or q.dtype != v.dtype or q.dtype not in ("f16", "bf16")):
+        raise ValueError(f"attention: q, k, v must all be f16 or all bf16, got {q.dtype}, {k.dtype}, {v.dtype}")
+    if v.dtype not in ("f16", "bf16"):
+        raise ValueError(f"attention: v must be f16 or bf16, got {v.dtype}")
+    kern = gpu.kernel("attention", "attention", HD=D, WM=wm, BK=bk, CAUSAL=int(causal), O_T=OUT_DT[out.dtype],
+                      QK8=int(q8), IN_T=OUT_DT[v.dtype], **variant)
+    sh = seq_heads or H
+    params = pack("7if3i", Lq, L, H, KVH, q_rows, k_rows, sh * D, scale * LOG2E, causal_off, sh, seq_rows)
+    gpu.launch(kern, None, None, [q, k, v, out, None, q_scale, k_scale], params, params_index=4)
+
+
+def attention_scores(gpu: Gpu, q: Tensor, k: Tensor, v: Tensor, scores: Tensor, *, Lq: int, L: int, H: int,
+                     KVH: int, D: int, q_rows: int, k_rows: int, q_scale: Tensor | None = None,
+                     k_scale: Tensor | None = None):
+    """Test hook (no reference counterpart): the raw score accumulators of attention's own MFMA path,
+    scores[h][i][j] = q_i . k_j (int32 for int8 inputs, f32 otherwise), for keys j < L."""
+    q8 = q_scale is not None
+    vt = v.dtype if v.dtype in ("f16", "bf16") else "bf16"
+    kern = gpu.kernel("attention", "attention_scores", HD=D, QK8=int(q8), IN_T=OUT_DT[vt])
+    params = pack("7if3i", Lq, L, H, KVH, q_rows, k_rows, H * D, 1.0, 0, H, 0)
+    gpu.launch(kern, None, None, [q, k, v, scores, None, q_scale, k_scale], params, params_index=4)
+
+
+def qk_norm_rope(gpu: Gpu, qkv: Tensor, wq: Tensor | None, wk: Tensor | None, cos: Tensor | None,
+                 sin: Tensor | None, Q: Tensor, K: Tensor, V: Tensor, *, M: int, Hq: int, Hk: int, Hv: int,
+                 hd: int, out_rows: int, rot: int, eps: float, norm: bool = True, in_stride: int | None = None,
+                 seq_len: int | None = None, q_scale: Tensor | None = None, k_scale: Tensor | None = None,
+                 qk_rot: bool = False):
+    """Per-head RMS norm and rotary embedding of queries and keys, split into head-major Q, K, V.
+
+    qk_rot (with int8 outputs): queries and keys rotated by the same orthonormal Walsh-Hadamard matrix with
+    fixed signs before their int8 rounding; their products, and attention, are unchanged, the rounding loses
+    less. Q, K [heads][out_rows][hd] (i8 with q_scale / k_scale [heads][out_rows], else f16 / bf16), V likewise
+    (f16 / bf16)."""
+    q8 = int(q_scale is not None)
+    if q8 and (Q.dtype != "i8" or K.dtype != "i8" or k_scale is None):
+        raise ValueError("qk_norm_rope: int8 outputs need i8 Q and K and both scale tensors")
+    qk_t = "half" if q8 else OUT_DT[Q.dtype]
+    k = gpu.kernel("ops", "qk_norm_rope", NSG=8, HDIM=hd, IN_T=OUT_DT[qkv.dtype], QK8=q8,
+                   QKROT=int(qk_rot and q8), QK_T=qk_t, V_T=OUT_DT[V.dtype])
+    slots = Hq + Hk + Hv
+    params = pack("8ifi", M, Hq, Hk, Hv, in_stride or slots * hd, out_rows, rot, int(norm), eps, seq_len or M)
+    gpu.launch(k, None, None, [qkv, wq, wk, cos, sin, Q, K, V, None, q_scale, k_scale], params, params_index=8)

@@ -1,0 +1,318 @@
+"""The gfx950 attention kernels against the CPU oracle.
+
+* int32 score accumulators of the int8 path: bit-exact against exact integer products (through attention's own
+  MFMA path and LDS staging: ops.attention_scores).
+* Outputs: the reference's own cases (tests/test_attention.py: check :23-56 with half inputs, check_q8 :60-114
+  with int8 scores, temp/ramp stresses, GQA, causal, D=64) with its tolerance 5e-3 max-abs against float64;
+  the north-star tolerance (2e-2 max-abs, 1e-3 mean-abs against fp32/float64) for the bf16 paths and the
+  BASELINE configs.
+"""
+
+import numpy as np
+import pytest
+
+from h3metal_amd import ops
+from oracle import attention as oa
+from oracle import prepass as op
+from oracle.bf16 import from_bf16, to_bf16
+
+pytestmark = pytest.mark.gpu
+
+NS_MAX, NS_MEAN = 2e-2, 1e-3
+
+
+def q8(x):
+    """Per-row symmetric int8 of tests/test_attention.py:74-76."""
+    s = np.abs(x).max(-1, keepdims=True) / 127
+    return np.rint(x / s).astype(np.int8), s[..., 0].astype(np.float32)
+
+
+def padded(gpu, arr, rows, dtype):
+    t = gpu.empty((arr.shape[0], rows) + arr.shape[2:], dtype)
+    full = np.zeros((arr.shape[0], rows) + arr.shape[2:], arr.dtype)
+    full[:, :arr.shape[1]] = arr
+    t.write(full)
+    return t
+
+
+def run_attention(gpu, q, k, v, *, dtype, Lq, L, H, KVH, D, scale, causal=False, off=0, qs=None, ks=None,
+                  out_dt="f16", q_rows=None, k_rows=None, seq_heads=None, seq_rows=0, out_rows=None):
+    q_rows = q_rows or (Lq + 63) // 64 * 64
+    k_rows = k_rows or (L + 31) // 32 * 32
+    print(f"[attention] Lq={Lq} L={L} H={H} KVH={KVH} D={D} dtype={dtype} causal={causal} q8={qs is not None} "
+          f"out={out_dt}", flush=True)
+    qdt = "i8" if qs is not None else dtype
+    Q, K, V = padded(gpu, q, q_rows, qdt), padded(gpu, k, k_rows, qdt), padded(gpu, v, k_rows, dtype)
+    sh = seq_heads or H
+    rows = out_rows or q_rows
+    O = gpu.empty((rows, sh * D), out_dt)
+    extra = {}
+    if qs is not None:
+        extra = dict(q_scale=padded(gpu, qs, q_rows, "f32"), k_scale=padded(gpu, ks, k_rows, "f32"))
+    ops.attention(gpu, Q, K, V, O, Lq=Lq, L=L, H=H, KVH=KVH, D=D, q_rows=q_rows, k_rows=k_rows, scale=scale,
+                  causal=causal, causal_off=off, seq_heads=seq_heads, seq_rows=seq_rows, **extra)
+    gpu.wait()
+    o = O.numpy()
+    return from_bf16(o) if out_dt == "bf16" else o.astype(np.float64)
+
+
+# -- int32 / fp32 score accumulators -------------------------------------------------------------------------------
+
+@pytest.mark.parametrize("Lq,L,H,KVH,D", [(100, 100, 2, 2, 128), (77, 300, 3, 3, 128), (64, 64, 4, 1, 64),
+                                          (300, 1037, 2, 1, 128), (1, 5, 1, 1, 128)])
+def test_int32_scores_bit_exact(gpu, Lq, L, H, KVH, D):
+    rng = np.random.default_rng(Lq + L)
+    qi = rng.integers(-127, 128, (H, Lq, D)).astype(np.int8)
+    ki = rng.integers(-127, 128, (KVH, L, D)).astype(np.int8)
+    qi[0, 0] = -127  # extreme magnitudes: 128 * 127^2 must not overflow or round
+    ki[0, 0] = -127
+    q_rows, k_rows = (Lq + 63) // 64 * 64, (L + 31) // 32 * 32
+    Q, K = padded(gpu, qi, q_rows, "i8"), padded(gpu, ki, k_rows, "i8")
+    V = gpu.empty((KVH, k_rows, D), "bf16")
+    qs, ks = gpu.upload(np.ones((H, q_rows), np.float32)), gpu.upload(np.ones((KVH, k_rows), np.float32))
+    S = gpu.empty((H, Lq, L), "i32")
+    ops.attention_scores(gpu, Q, K, V, S, Lq=Lq, L=L, H=H, KVH=KVH, D=D, q_rows=q_rows, k_rows=k_rows,
+                         q_scale=qs, k_scale=ks)
+    gpu.wait()
+    want = oa.int_scores(qi, ki, H_per_kv=H // KVH)
+    got = S.numpy()
+    assert np.array_equal(got, want), f"{(got != want).sum()} int32 scores differ"
+
+
+def test_int32_scores_golden_fixture(gpu):
+    import os
+    f = np.load(os.path.join(os.path.dirname(__file__), "golden", "scores_int8.npz"))
+    qi, ki, want = f["Q"], f["K"], f["S"]
+    H, Lq, D = qi.shape
+    L = ki.shape[1]
+    Q, K = padded(gpu, qi, 64, "i8"), padded(gpu, ki, 64, "i8")
+    S = gpu.empty((H, Lq, L), "i32")
+    ops.attention_scores(gpu, Q, K, gpu.empty((H, 64, D), "bf16"), S, Lq=Lq, L=L, H=H, KVH=H, D=D, q_rows=64,
+                         k_rows=64, q_scale=gpu.upload(np.ones((H, 64), np.float32)),
+                         k_scale=gpu.upload(np.ones((H, 64), np.float32)))
+    gpu.wait()
+    assert np.array_equal(S.numpy(), want)
+
+
+@pytest.mark.parametrize("dtype", ["bf16", "f16"])
+def test_float_scores(gpu, dtype):
+    """16-bit inputs: products are exact in fp32 and the 128-term sums are accumulated in fp32."""
+    rng = np.random.default_rng(5)
+    H, Lq, L, D = 2, 70, 130, 128
+    q = rng.standard_normal((H, Lq, D)).astype(np.float32)
+    k = rng.standard_normal((H, L, D)).astype(np.float32)
+    if dtype == "bf16":
+        qh, kh, qf, kf = to_bf16(q), to_bf16(k), from_bf16(to_bf16(q)), from_bf16(to_bf16(k))
+    else:
+        qh, kh = q.astype(np.float16), k.astype(np.float16)
+        qf, kf = qh.astype(np.float32), kh.astype(np.float32)
+    Q, K = padded(gpu, qh, 128, dtype), padded(gpu, kh, 160, dtype)
+    S = gpu.empty((H, Lq, L), "f32")
+    ops.attention_scores(gpu, Q, K, gpu.empty((H, 160, D), dtype), S, Lq=Lq, L=L, H=H, KVH=H, D=D, q_rows=128,
+                         k_rows=160)
+    gpu.wait()
+    want = np.einsum("hqd,hkd->hqk", qf.astype(np.float64), kf.astype(np.float64))
+    np.testing.assert_allclose(S.numpy(), want, rtol=0, atol=1e-3)
+
+
+# -- outputs: the reference's tests/test_attention.py cases --------------------------------------------------------
+
+CHECK_CASES = [(100, 100, 2, 2, 128, False), (77, 300, 3, 3, 128, False), (64, 64, 4, 1, 64, False),
+               (130, 130, 8, 2, 128, True), (1000, 1037, 2, 2, 128, False)]
+
+
+@pytest.mark.parametrize("Lq,L,H,KVH,D,causal", CHECK_CASES)
+def test_half_path_reference_cases(gpu, Lq, L, H, KVH, D, causal):
+    """check() of tests/test_attention.py:23-42: half Q/K/V ~N(0,1), seed 0, max-abs < 5e-3 vs float64."""
+    rng = np.random.default_rng(0)
+    q = rng.standard_normal((H, Lq, D)).astype(np.float16)
+    k = rng.standard_normal((KVH, L, D)).astype(np.float16)
+    v = rng.standard_normal((KVH, L, D)).astype(np.float16)
+    got = run_attention(gpu, q, k, v, dtype="f16", Lq=Lq, L=L, H=H, KVH=KVH, D=D, scale=D ** -0.5, causal=causal)
+    ref = oa.ref_attention(q, k, v, D ** -0.5, causal=causal)
+    err = np.abs(got[:Lq] - ref).max()
+    assert err < 5e-3, err
+
+
+Q8_CASES = [dict(Lq=100, L=100, H=2, KVH=2, D=128), dict(Lq=300, L=1037, H=3, KVH=3, D=128),
+            dict(Lq=130, L=130, H=8, KVH=2, D=128, causal=True), dict(Lq=64, L=64, H=4, KVH=4, D=64),
+            dict(Lq=300, L=1037, H=3, KVH=3, D=128, temp=6.0),
+            dict(Lq=257, L=4100, H=2, KVH=2, D=128, temp=8.0, ramp=4.0),
+            dict(Lq=200, L=200, H=2, KVH=2, D=128, causal=True, temp=5.0, ramp=3.0)]
+
+
+@pytest.mark.parametrize("case", Q8_CASES, ids=lambda c: "-".join(f"{k}{v}" for k, v in c.items()))
+@pytest.mark.parametrize("vdt", ["f16", "bf16"])
+def test_int8_path_reference_cases(gpu, case, vdt):
+    """check_q8() of tests/test_attention.py:60-114: int8 scores against float64 attention of the dequantised
+    inputs; max-abs < 5e-3 with half V (the reference's bound), the north-star bound with bf16 V."""
+    c = dict(case)
+    Lq, L, H, KVH, D = c["Lq"], c["L"], c["H"], c["KVH"], c["D"]
+    causal, temp, ramp = c.get("causal", False), c.get("temp", 1.0), c.get("ramp", 0.0)
+    rng = np.random.default_rng(0)
+    q = rng.standard_normal((H, Lq, D)).astype(np.float32) * temp
+    k = rng.standard_normal((KVH, L, D)).astype(np.float32)
+    if ramp:
+        k *= (1 + ramp * np.arange(L) / L)[None, :, None].astype(np.float32)
+    v = rng.standard_normal((KVH, L, D)).astype(np.float16)
+    qi, qs = q8(q)
+    ki, ks = q8(k)
+    vh = v if vdt == "f16" else to_bf16(v.astype(np.float32))
+    vf = v.astype(np.float64) if vdt == "f16" else from_bf16(vh).astype(np.float64)
+    got = run_attention(gpu, qi, ki, vh, dtype=vdt, Lq=Lq, L=L, H=H, KVH=KVH, D=D, scale=D ** -0.5, causal=causal,
+                        qs=qs, ks=ks, q_rows=(Lq + 255) // 256 * 256)
+    ref = oa.ref_attention(qi * qs[..., None].astype(np.float64), ki * ks[..., None].astype(np.float64), vf,
+                           D ** -0.5, causal=causal)
+    err = np.abs(got[:Lq] - ref)
+    if vdt == "f16":
+        assert err.max() < 5e-3, err.max()
+    else:
+        assert err.max() < NS_MAX and err.mean() < NS_MEAN, (err.max(), err.mean())
+
+
+@pytest.mark.parametrize("out_dt", ["bf16", "f32"])
+def test_bf16_path_and_output_types(gpu, out_dt):
+    rng = np.random.default_rng(21)
+    H, Lq, L, D = 3, 333, 500, 128
+    q, k, v = (to_bf16(rng.standard_normal((H, n, D)).astype(np.float32)) for n in (Lq, L, L))
+    got = run_attention(gpu, q, k, v, dtype="bf16", Lq=Lq, L=L, H=H, KVH=H, D=D, scale=D ** -0.5, out_dt=out_dt)
+    ref = oa.ref_attention(from_bf16(q), from_bf16(k), from_bf16(v), D ** -0.5)
+    err = np.abs(got[:Lq] - ref)
+    assert err.max() < NS_MAX and err.mean() < NS_MEAN, (err.max(), err.mean())
+    if out_dt == "f32":
+        assert err.max() < 5e-3
+
+
+def test_batched_sequences_output_placement(gpu):
+    """seq_heads / seq_rows (attention.metal:384-385; the VAE's batched tiles, vae.py:206-207): 6 heads as 3
+    sequences of 2 heads, each sequence's rows seq_rows apart."""
+    rng = np.random.default_rng(22)
+    H, sh, Lq, D, seq_rows = 6, 2, 40, 64, 48
+    q, k, v = (rng.standard_normal((H, Lq, D)).astype(np.float16) for _ in range(3))
+    got = run_attention(gpu, q, k, v, dtype="f16", Lq=Lq, L=Lq, H=H, KVH=H, D=D, scale=D ** -0.5, seq_heads=sh,
+                        seq_rows=seq_rows, out_rows=3 * seq_rows)
+    ref = oa.ref_attention(q, k, v, D ** -0.5, seq_heads=sh, seq_rows=seq_rows)
+    for s in range(3):
+        blk = slice(s * seq_rows, s * seq_rows + Lq)
+        assert np.abs(got[blk] - ref[blk]).max() < 5e-3
+    assert (got[Lq:seq_rows] == 0).all()  # rows between sequences untouched
+
+
+def test_causal_offset(gpu):
+    rng = np.random.default_rng(23)
+    H, Lq, L, D, off = 2, 90, 150, 128, 60
+    q, k, v = (rng.standard_normal((H, n, D)).astype(np.float16) for n in (Lq, L, L))
+    got = run_attention(gpu, q, k, v, dtype="f16", Lq=Lq, L=L, H=H, KVH=H, D=D, scale=D ** -0.5, causal=True,
+                        off=off)
+    ref = oa.ref_attention(q, k, v, D ** -0.5, causal=True, off=off)
+    assert np.abs(got[:Lq] - ref).max() < 5e-3
+
+
+# -- BASELINE configs ------------------------------------------------------------------------------------------------
+
+def test_config1_plumbing(gpu):
+    """Config 1: B=1, H=4, S=256, D=128, fp32 N(0,1), scale 1/sqrt(128), no mask, vs the numpy reference of the
+    fp32 inputs (the kernel takes them as bf16)."""
+    rng = np.random.default_rng(0)
+    H, S, D = 4, 256, 128
+    q, k, v = (rng.standard_normal((H, S, D)).astype(np.float32) for _ in range(3))
+    got = run_attention(gpu, to_bf16(q), to_bf16(k), to_bf16(v), dtype="bf16", Lq=S, L=S, H=H, KVH=H, D=D,
+                        scale=D ** -0.5, out_dt="f32")
+    ref = oa.ref_attention(q, k, v, D ** -0.5)
+    err = np.abs(got[:S] - ref)
+    assert err.max() < NS_MAX and err.mean() < NS_MEAN, (err.max(), err.mean())
+
+
+def axial_rope_tables(n_txt, grid, hd, theta=10000.0):
+    """2D axial RoPE angles per row for the bf16 FLUX-shaped config: text rows angle 0; image rows rotate half of
+    the rotated pairs by the row coordinate and half by the column coordinate (flux2.py:396-401)."""
+    half = hd // 2
+    per_axis = half // 2
+    freqs = theta ** (-np.arange(per_axis) / per_axis)
+    rows = np.zeros((n_txt + grid * grid, half))
+    yy, xx = np.divmod(np.arange(grid * grid), grid)
+    rows[n_txt:, :per_axis] = yy[:, None] * freqs
+    rows[n_txt:, per_axis:] = xx[:, None] * freqs
+    return np.cos(rows).astype(np.float32), np.sin(rows).astype(np.float32)
+
+
+def test_config2_flux_joint_bf16(gpu):
+    """Config 2 (FLUX.2-klein-4B joint attention): H=24, D=128, S=4608 (512 text + 64x64 image), bf16 N(0,1),
+    per-head RMSNorm on Q/K and 2D axial RoPE through qk_norm_rope, unquantised bf16 attention. Checked on a
+    seeded sample of query rows against float64 attention of the kernel's own bf16 Q/K/V."""
+    rng = np.random.default_rng(2)
+    H, D, n_txt, grid = 24, 128, 512, 64
+    S = n_txt + grid * grid
+    x = to_bf16(rng.standard_normal((S, 3 * H * D)).astype(np.float32))
+    cs, sn = axial_rope_tables(n_txt, grid, D)
+    g = gpu
+    X = g.upload(x, "bf16")
+    Q, K, V = (g.empty((H, S, D), "bf16") for _ in range(3))
+    ones = g.upload(np.ones(D, np.float32))
+    ops.qk_norm_rope(g, X, ones, ones, g.upload(cs), g.upload(sn), Q, K, V, M=S, Hq=H, Hk=H, Hv=H, hd=D,
+                     out_rows=S, rot=D, eps=1e-6, norm=True)
+    O = g.empty((S, H * D), "bf16")
+    ops.attention(g, Q, K, V, O, Lq=S, L=S, H=H, KVH=H, D=D, q_rows=S, k_rows=S, scale=D ** -0.5)
+    g.wait()
+    qh, kh, vh = (from_bf16(t.numpy()).astype(np.float64) for t in (Q, K, V))
+    # the pre-pass output itself against the float32 oracle (bf16 rounding of the oracle's result)
+    rows = np.sort(rng.choice(S, 256, replace=False))
+    want = op.qk_norm_rope(from_bf16(x[rows]), Hq=H, Hk=H, Hv=H, hd=D, out_rows=len(rows), rot=D, eps=1e-6,
+                           norm=True, wq=np.ones(D, np.float32), wk=np.ones(D, np.float32), cs=cs[rows], sn=sn[rows])
+    assert np.array_equal(Q.numpy()[:, rows], to_bf16(want["Q"]))
+    got = from_bf16(O.numpy()).astype(np.float64)
+    ref = oa.ref_attention(qh[:, rows], kh, vh, D ** -0.5)
+    err = np.abs(got[rows] - ref)
+    assert err.max() < NS_MAX and err.mean() < NS_MEAN, (err.max(), err.mean())
+
+
+def test_config3_zimage_key_padding(gpu):
+    """Config 3 (Z-Image-Turbo): H=30, D=128, 4096 image rows then text padded to 512 with only the first
+    L_txt ~ U[32, 512] valid: the boolean key mask is keys >= 4096 + L_txt (the kernel's L). The padded key rows
+    hold N(0,1) data here, which the mask must ignore."""
+    rng = np.random.default_rng(3)
+    H, D, n_img = 30, 128, 4096
+    L_txt = int(rng.integers(32, 513))
+    S = n_img + 512
+    L = n_img + L_txt
+    q, k, v = (to_bf16(rng.standard_normal((H, S, D)).astype(np.float32)) for _ in range(3))
+    Q, K, V = (gpu.upload(t, "bf16") for t in (q, k, v))
+    O = gpu.empty((S, H * D), "bf16")
+    ops.attention(gpu, Q, K, V, O, Lq=S, L=L, H=H, KVH=H, D=D, q_rows=S, k_rows=S, scale=D ** -0.5)
+    gpu.wait()
+    rows = np.sort(rng.choice(S, 192, replace=False))
+    ref = oa.ref_attention(from_bf16(q[:, rows]), from_bf16(k), from_bf16(v), D ** -0.5, L=L)
+    err = np.abs(from_bf16(O.numpy())[rows] - ref)
+    assert err.max() < NS_MAX and err.mean() < NS_MEAN, (err.max(), err.mean(), L_txt)
+
+
+def test_config4_int8_rotated_full_size(gpu):
+    """Config 4 at full size: H=32, D=128, S=16896, outlier channels x20, rotation + int8 pre-pass, int8
+    attention with bf16 V. Checked on a seeded sample of query rows against float64 attention of the dequantised
+    int8 inputs (the reference's check_q8 convention) and, within the rotation's gain, against fp32 attention of
+    the unquantised bf16 inputs; int32 scores of sampled rows bit-exact."""
+    rng = np.random.default_rng(4)
+    H, D, S = 32, 128, 16896
+    x = rng.standard_normal((S, 3, H, D)).astype(np.float32)
+    for part in (0, 1):
+        for h in range(H):
+            x[:, part, h, rng.choice(D, 4, replace=False)] *= 20
+    xb = to_bf16(x.reshape(S, 3 * H * D))
+    X = gpu.upload(xb, "bf16")
+    Q, K = gpu.empty((H, S, D), "i8"), gpu.empty((H, S, D), "i8")
+    V = gpu.empty((H, S, D), "bf16")
+    qs, ks = gpu.empty((H, S), "f32"), gpu.empty((H, S), "f32")
+    ops.qk_norm_rope(gpu, X, None, None, None, None, Q, K, V, M=S, Hq=H, Hk=H, Hv=H, hd=D, out_rows=S, rot=0,
+                     eps=1e-6, norm=False, q_scale=qs, k_scale=ks, qk_rot=True)
+    O = gpu.empty((S, H * D), "bf16")
+    ops.attention(gpu, Q, K, V, O, Lq=S, L=S, H=H, KVH=H, D=D, q_rows=S, k_rows=S, scale=D ** -0.5, q_scale=qs,
+                  k_scale=ks)
+    gpu.wait()
+    qi, ki, qsh, ksh, vh = Q.numpy(), K.numpy(), qs.numpy(), ks.numpy(), from_bf16(V.numpy())
+    rows = np.sort(rng.choice(S, 128, replace=False))
+    qd = qi[:, rows] * qsh[:, rows, None].astype(np.float64)
+    kd = ki * ksh[..., None].astype(np.float64)
+    ref = oa.ref_attention(qd, kd, vh, D ** -0.5)
+    got = from_bf16(O.numpy()).astype(np.float64)[rows]
+    err = np.abs(got - ref)
+    assert err.max() < NS_MAX and err.mean() < NS_MEAN, (err.max(), err.mean())

@@ -1,0 +1,120 @@
+"""Host-side logic on the CPU: the C-ABI library loads and exports every symbol include/h3hip.h declares, the
+Python launchers pack the reference's parameter blocks and buffer orders (h3metal/ops.py:177-191, 225-239), and
+the runtime fails cleanly without a GPU. No kernel runs here."""
+
+import ctypes
+import os
+import re
+import struct
+
+import numpy as np
+import pytest
+
+from h3metal_amd import gpu as G
+from h3metal_amd import ops
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def header_functions():
+    text = open(os.path.join(ROOT, "include", "h3hip.h")).read()
+    text = re.sub(r"//.*", "", text)
+    return sorted(set(re.findall(r"\b(h3_\w+)\s*\(", text)))
+
+
+def test_library_exports_every_header_symbol():
+    lib = ctypes.CDLL(G._find_library())
+    names = header_functions()
+    assert len(names) >= 20
+    for n in names:
+        assert hasattr(lib, n), n
+    # and gpu.py binds exactly those
+    assert sorted(G.SIGNATURES) == names
+
+
+def test_open_without_gpu_fails_cleanly():
+    if os.path.exists("/dev/kfd") and os.environ.get("HIP_VISIBLE_DEVICES", "") != "-1":
+        pytest.skip("a GPU may be present")
+    with pytest.raises(G.GpuError, match="device"):
+        G.Gpu()
+
+
+class FakeGpu:
+    """Records what a launcher asks the runtime for."""
+
+    def __init__(self):
+        self.kernels, self.launches = [], []
+
+    def kernel(self, file, fn, **macros):
+        self.kernels.append((file, fn, macros))
+        return (file, fn, tuple(sorted(macros.items())))
+
+    def launch(self, k, grid, threads, args, params=b"", params_index=None, tg_mem=0):
+        self.launches.append((k, args, params, params_index))
+
+
+def T(shape, dtype):
+    return G.Tensor(G.Buffer(0, 0), 0, tuple(shape), dtype)
+
+
+def test_attention_launcher_packs_reference_params():
+    g = FakeGpu()
+    q, k = T((32, 256, 128), "i8"), T((32, 256, 128), "i8")
+    v, o = T((32, 256, 128), "bf16"), T((256, 32 * 128), "bf16")
+    qs, ks = T((32, 256), "f32"), T((32, 256), "f32")
+    ops.attention(g, q, k, v, o, Lq=250, L=249, H=32, KVH=32, D=128, q_rows=256, k_rows=256, scale=128 ** -0.5,
+                  wm=10, bk=32, DB=1, PVORDER=1, VX=1, TG=3, q_scale=qs, k_scale=ks)
+    (file, fn, macros), = g.kernels
+    assert (file, fn) == ("attention", "attention")
+    assert macros["QK8"] == 1 and macros["O_T"] == "bfloat" and macros["HD"] == 128 and "TG" not in macros
+    (_, args, params, pi), = g.launches
+    assert pi == 4 and args[4] is None and args[5] is qs and args[6] is ks and args[:4] == [q, k, v, o]
+    vals = struct.unpack("<7if3i", params)
+    assert vals[:7] == (250, 249, 32, 32, 256, 256, 32 * 128) and vals[8:] == (0, 32, 0)
+    assert abs(vals[7] - 128 ** -0.5 * 1.4426950408889634) < 1e-7  # scale in log2 units (ops.py:188)
+
+
+def test_attention_launcher_rejects_mixed_types():
+    g = FakeGpu()
+    with pytest.raises(ValueError):
+        ops.attention(g, T((1, 64, 128), "f16"), T((1, 64, 128), "bf16"), T((1, 64, 128), "f16"),
+                      T((64, 128), "f16"), Lq=64, L=64, H=1, KVH=1, D=128, q_rows=64, k_rows=64, scale=0.1)
+    with pytest.raises(ValueError):
+        ops.attention(g, T((1, 64, 128), "i8"), T((1, 64, 128), "i8"), T((1, 64, 128), "f16"),
+                      T((64, 128), "f16"), Lq=64, L=64, H=1, KVH=1, D=128, q_rows=64, k_rows=64, scale=0.1,
+                      q_scale=T((1, 64), "f32"))
+
+
+def test_qk_norm_rope_launcher_packs_reference_params():
+    g = FakeGpu()
+    qkv = T((100, 3 * 4 * 128), "bf16")
+    Q, K, V = T((4, 128, 128), "i8"), T((4, 128, 128), "i8"), T((4, 128, 128), "bf16")
+    qs, ks = T((4, 128), "f32"), T((4, 128), "f32")
+    ops.qk_norm_rope(g, qkv, None, None, None, None, Q, K, V, M=100, Hq=4, Hk=4, Hv=4, hd=128, out_rows=128,
+                     rot=96, eps=1e-6, norm=False, q_scale=qs, k_scale=ks, qk_rot=True)
+    (file, fn, macros), = g.kernels
+    assert (file, fn) == ("ops", "qk_norm_rope") and macros["QK8"] == 1 and macros["QKROT"] == 1
+    assert macros["IN_T"] == "bfloat" and macros["V_T"] == "bfloat" and macros["HDIM"] == 128
+    (_, args, params, pi), = g.launches
+    assert pi == 8 and len(args) == 11 and args[8] is None and args[9] is qs and args[10] is ks
+    vals = struct.unpack("<8ifi", params)
+    assert vals[:8] == (100, 4, 4, 4, 12 * 128, 128, 96, 0) and vals[9] == 100
+    # qk_rot without int8 outputs is ignored, as in the reference (QKROT=int(qk_rot and q8), ops.py:233)
+    g2 = FakeGpu()
+    ops.qk_norm_rope(g2, qkv, None, None, None, None, T((4, 128, 128), "f16"), T((4, 128, 128), "f16"), V, M=100,
+                     Hq=4, Hk=4, Hv=4, hd=128, out_rows=128, rot=0, eps=1e-6, qk_rot=True)
+    assert g2.kernels[0][2]["QKROT"] == 0 and g2.kernels[0][2]["QK_T"] == "half"
+
+
+def test_pack_and_pad_rows():
+    assert len(G.pack("7if3i", *range(7), 1.0, 0, 1, 2)) == 44  # sizeof(AttnParams), csrc/h3hip_internal.h
+    assert len(G.pack("8ifi", *range(8), 1e-6, 5)) == 40         # sizeof(QkRopeParams)
+    assert ops.pad_rows(16684) == 16768 and ops.pad_rows(16896) == 16896 and ops.pad_rows(1, 64) == 64
+
+
+def test_tensor_views():
+    t = T((10, 4), "f16")
+    r = t.row(3, 2)
+    assert r.offset == 3 * 4 * 2 and r.shape == (2, 4)
+    v = t.view((5, 8), "i8", offset_elems=4)
+    assert v.offset == 8 and v.dtype == "i8" and v.nbytes == 40
