@@ -14,32 +14,44 @@
 //   the end (:376-393).
 //
 // The gfx950 design (not the Metal one):
-//  * One workgroup = NW waves of 64 lanes; each wave owns 32 query rows of one
-//    head and the workgroup walks the keys in blocks of BK = 64, staged in LDS
-//    (double-buffered: the next block's global loads are in flight during this
-//    block's math). The 1-D grid is remapped so that each XCD (own L2) runs a
-//    contiguous range of (head, query-block) tiles: the tiles of one head share
-//    its K/V stream in that XCD's L2.
+//  * A workgroup is 8 waves in two groups of 4 (waves w and w + 4 share a SIMD).
+//    Each wave owns 32 query rows of one head (256 per workgroup); the
+//    workgroup walks the keys in blocks of BK = 64 staged in LDS.
+//  * Ping-pong: every key block is two half-steps separated by workgroup
+//    barriers. In a half-step one group runs its matrix phase (the score
+//    MFMAs of block j and the P V MFMAs of block j-1) while the other group
+//    runs its vector phase (the softmax of its block), then they swap. MFMA
+//    and VALU work of the two waves on a SIMD overlap this way; a single
+//    wave interleaving both does not overlap them well on CDNA4.
 //  * Scores are computed transposed, S^T = K Q^T, on the 32x32 MFMA
-//    (v_mfma_i32_32x32x32_i8 or v_mfma_f32_32x32x16_{bf16,f16}): an accumulator
-//    lane then holds 16 keys of ONE query (column = lane % 32), so the softmax
-//    state (max, sum, rescale) is per lane and only the partner lane (lane ^ 32,
-//    same query, other keys) ever has to be consulted.
-//  * The K rows of a 32-key tile are fed to the MFMA in the order
+//    (v_mfma_i32_32x32x32_i8 or v_mfma_f32_32x32x16_{bf16,f16}): an
+//    accumulator lane holds 16 keys of ONE query (column = lane % 32), so the
+//    softmax state (max, sum, rescale) is per lane; only the partner lane
+//    (lane ^ 32, same query, other keys) is ever consulted.
+//  * K rows of a 32-key tile are fed to the score MFMA in the order
 //    pi(a) = 16*(a/16) + 8*((a/4)%2) + 4*((a/8)%2) + a%4, so that accumulator
 //    element i of lane-half h holds key 16*(i/8) + 8*h + i%8: each half of the
-//    accumulator is then, as it stands, the B operand (8 consecutive keys per
-//    lane) of one 32x32x16 P V MFMA computing O^T = V^T P^T. O^T lands with the
-//    same lane = query layout, so rescaling O is a per-lane multiply.
-//  * V is stored transposed in LDS (V^T[d][key], 16-byte pieces XOR-swizzled by
-//    d % 8) so that each P V operand is one 16-byte LDS read; K rows are
-//    swizzled by key bits so that the permuted row reads are bank-conflict free.
+//    accumulator is, as it stands, the B operand (8 consecutive keys per lane)
+//    of one 32x32x16 P V MFMA computing O^T = V^T P^T, and O^T lands with the
+//    same lane = query layout (rescaling O is a per-lane multiply).
+//  * V stays row-major in LDS; its MFMA operand (4 keys x 1 channel per
+//    read) comes from the transposing LDS read ds_read_b64_tr_b16: in each
+//    16-lane group, source lane l addresses V[K0 + l/4][D0 + 4*(l%4) .. +3] and
+//    destination lane i receives V[K0 .. K0+3][D0 + i]. V rows are swizzled in
+//    32-byte units by key % 4 and K rows in 16-byte pieces by key bits 0, 1, 3,
+//    so both LDS read patterns are bank-conflict free.
+//  * Global loads are unconditional (rows clamped, out-of-range rows zeroed
+//    after the load) so the compiler can count outstanding loads exactly;
+//    the next block's loads are issued at the start of a key block and land in
+//    LDS at the end of its second half-step.
+//  * The 1-D grid is remapped so that each XCD (own L2) runs a contiguous
+//    range of (head, query-block) tiles, which then share one head's K/V in L2.
 #include "h3hip_internal.h"
 
 #include <cfloat>
+#include <cmath>
 #include <cstring>
 #include <type_traits>
-#include <cmath>
 
 namespace h3 {
 namespace {
@@ -48,21 +60,25 @@ typedef int i32x4 __attribute__((ext_vector_type(4)));
 typedef int i32x16 __attribute__((ext_vector_type(16)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
-typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
+typedef short i16x4 __attribute__((ext_vector_type(4)));
+typedef short i16x8 __attribute__((ext_vector_type(8)));
 typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 
 enum { T_I8 = 0, T_BF16 = 1, T_F16 = 2, T_F32 = 3 };
 
 constexpr int BK = 64;         // keys per LDS block
+constexpr int NW = 8;          // waves per workgroup (two groups of 4)
 constexpr float SLACK = 8.0f;  // log2 units the running maximum may lag behind a score
 
 template <int T> struct Vec8;
-template <> struct Vec8<T_BF16> { using type = bf16x8; using elem = __bf16; };
-template <> struct Vec8<T_F16> { using type = f16x8; using elem = _Float16; };
+template <> struct Vec8<T_BF16> { using type = bf16x8; using pair = bf16x2; using elem = __bf16; };
+template <> struct Vec8<T_F16> { using type = f16x8; using pair = f16x2; using elem = _Float16; };
 
-// 32x32 product with a 16-byte A and B operand per lane.
+// 32x32 score product with a 16-byte A and B operand per lane.
 template <int QKT>
 __device__ __forceinline__ auto mma_qk(i32x4 a, i32x4 b, typename std::conditional<QKT == T_I8, i32x16, f32x16>::type c) {
   if constexpr (QKT == T_I8) {
@@ -77,9 +93,21 @@ __device__ __forceinline__ auto mma_qk(i32x4 a, i32x4 b, typename std::condition
 }
 
 template <int VT>
-__device__ __forceinline__ f32x16 mma_pv(typename Vec8<VT>::type a, typename Vec8<VT>::type b, f32x16 c) {
-  if constexpr (VT == T_BF16) return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
-  else return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+__device__ __forceinline__ f32x16 mma_pv(i16x8 a, typename Vec8<VT>::type b, f32x16 c) {
+  if constexpr (VT == T_BF16) return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a), b, c, 0, 0, 0);
+  else return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a), b, c, 0, 0, 0);
+}
+
+// Sum of a packed pair plus an accumulator (v_dot2_f32_{bf16,f16} with (1, 1)).
+template <int VT>
+__device__ __forceinline__ float sum2(typename Vec8<VT>::pair p, float acc) {
+  if constexpr (VT == T_BF16) return __builtin_amdgcn_fdot2_f32_bf16(p, bf16x2{(__bf16)1.0f, (__bf16)1.0f}, acc, false);
+  else return __builtin_amdgcn_fdot2(p, f16x2{(_Float16)1.0f, (_Float16)1.0f}, acc, false);
+}
+
+__device__ __forceinline__ i16x4 lds_tr16(const char *p) {
+  typedef __attribute__((address_space(3))) i16x4 *LP;
+  return __builtin_amdgcn_ds_read_tr16_b64_v4i16((LP)p);
 }
 
 // Swizzle of the 16-byte pieces of a K row in LDS: distinct for the 8 lanes
@@ -87,6 +115,12 @@ __device__ __forceinline__ f32x16 mma_pv(typename Vec8<VT>::type a, typename Vec
 template <int NP>
 __device__ __forceinline__ int kswz(int key) {
   return ((key & 3) | ((key >> 1) & 4)) & (NP - 1);
+}
+
+// Byte offset of 16-byte piece pc of V row `key` (32-byte units XOR key % 4).
+template <int D>
+__device__ __forceinline__ int voff(int key, int pc) {
+  return key * (D * 2) + ((((pc >> 1) ^ key) & 3) | ((pc >> 1) & ~3)) * 32 + (pc & 1) * 16;
 }
 
 template <int OT>
@@ -102,40 +136,42 @@ __device__ __forceinline__ void store4(char *dst, float a, float b, float c, flo
   }
 }
 
-template <int D, int QKT, int VT, int NW>
+template <int D, int QKT>
 struct Cfg {
   static constexpr bool QK8 = QKT == T_I8;
-  static constexpr int NT = NW * 64;         // threads
-  static constexpr int BQ = NW * 32;         // query rows per workgroup
-  static constexpr int ESZ = QK8 ? 1 : 2;    // bytes per Q/K element
-  static constexpr int RB = D * ESZ;         // bytes per Q/K row
-  static constexpr int NP = RB / 16;         // 16-byte pieces per Q/K row
-  static constexpr int NCH = NP / 2;         // score MFMAs per 32x32 tile (one piece per lane half each)
+  static constexpr int NT = NW * 64;             // threads
+  static constexpr int BQ = NW * 32;             // query rows per workgroup
+  static constexpr int ESZ = QK8 ? 1 : 2;        // bytes per Q/K element
+  static constexpr int RB = D * ESZ;             // bytes per Q/K row
+  static constexpr int NP = RB / 16;             // 16-byte pieces per Q/K row
+  static constexpr int NCH = NP / 2;             // score MFMAs per 32x32 tile (one piece per lane half each)
+  static constexpr int VP = D * 2 / 16;          // 16-byte pieces per V row
   static constexpr int KBYTES = BK * RB;
-  static constexpr int VBYTES = D * BK * 2;
-  static constexpr int SBYTES = QK8 ? BK * 4 : 0;
-  static constexpr int BUF = KBYTES + VBYTES + SBYTES;
-  static constexpr int LDS = 2 * BUF;
-  static constexpr int KPT = (BK * NP + NT - 1) / NT;   // K pieces staged per thread
-  static constexpr int NVT = (BK / 4) * (D / 8);        // V tasks: 4 keys x 8 channels
-  static constexpr int VPT = (NVT + NT - 1) / NT;
+  static constexpr int VBYTES = BK * D * 2;
+  static constexpr int KOFF = 0;                          // K ring: 2 blocks
+  static constexpr int VOFF = 2 * KBYTES;                 // V ring: 2 blocks
+  static constexpr int SOFF = VOFF + 2 * VBYTES;          // key-scale ring: 3 blocks
+  static constexpr int LDS = SOFF + (QK8 ? 3 * BK * 4 : 0);
   static_assert(D % 32 == 0 && D <= 128, "head dim");
 };
 
 // DUMP: instead of attention, write the raw score accumulators S[h][q][key]
 // (int32 for int8 inputs, fp32 otherwise) of the same MFMA path, for tests.
-template <int D, int QKT, int VT, int OT, bool CAUSAL, int NW, bool DUMP>
-__global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2, 2)))
-void attention_kernel(const char *__restrict__ Q, const char *__restrict__ K, const char *__restrict__ V,
-                      char *__restrict__ O, const float *__restrict__ qs, const float *__restrict__ ks, AttnParams p,
-                      int nqb) {
-  using C = Cfg<D, QKT, VT, NW>;
+template <int D, int QKT, int VT, int OT, bool CAUSAL, bool DUMP>
+__global__ __launch_bounds__(NW * 64) void attention_kernel(const char *__restrict__ Q, const char *__restrict__ K,
+                                                            const char *__restrict__ V, char *__restrict__ O,
+                                                            const float *__restrict__ qs,
+                                                            const float *__restrict__ ks, AttnParams p, int nqb) {
+  using C = Cfg<D, QKT>;
   using VT8 = typename Vec8<VT>::type;
   using VE = typename Vec8<VT>::elem;
+  using VP2 = typename Vec8<VT>::pair;
   using SAcc = typename std::conditional<C::QK8, i32x16, f32x16>::type;
   extern __shared__ __attribute__((aligned(16))) char smem[];
 
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, hl = lane >> 5, l32 = lane & 31;
+  const int tid = threadIdx.x, lane = tid & 63, hl = lane >> 5, l32 = lane & 31;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: keeps the group branches scalar
+  const int grp = w >> 2;  // 0: matrix phase first in each key block, 1: vector phase first
   // XCD-aware tile order: workgroup b runs on XCD b % 8; give each XCD a contiguous range.
   const int nb = gridDim.x, b = blockIdx.x;
   const int per = nb >> 3, rem = nb & 7, xcd = b & 7, loc = b >> 3;
@@ -150,8 +186,10 @@ void attention_kernel(const char *__restrict__ Q, const char *__restrict__ K, co
   {
     const char *qrow = Q + ((size_t)h * p.q_rows + (qvalid ? q : 0)) * C::RB;
 #pragma unroll
-    for (int c = 0; c < C::NCH; c++)
-      qreg[c] = qvalid ? *(const i32x4 *)(qrow + (2 * c + hl) * 16) : i32x4{0, 0, 0, 0};
+    for (int c = 0; c < C::NCH; c++) {
+      const i32x4 v = *(const i32x4 *)(qrow + (2 * c + hl) * 16);
+      qreg[c] = qvalid ? v : i32x4{0, 0, 0, 0};
+    }
   }
   float qsc = p.scale;
   if constexpr (C::QK8) qsc = qvalid ? fmaxf(qs[(size_t)h * p.q_rows + q] * p.scale, FLT_MIN) : 1.0f;
@@ -161,57 +199,60 @@ void attention_kernel(const char *__restrict__ Q, const char *__restrict__ K, co
   const float *ksh = C::QK8 ? ks + (size_t)kvh * p.k_rows : nullptr;
   int kend = p.L;
   if constexpr (CAUSAL) kend = min(p.L, qb * C::BQ + C::BQ + p.causal_off);
+  const int nblk = kend > 0 ? (kend + BK - 1) / BK : 0;
+  const int Lm1 = p.L - 1;
 
-  // staging registers for one key block
-  i32x4 kr[C::KPT];
-  u32x4 vr[C::VPT][4];
+  // -- staging: global -> registers -> LDS. Group g stages rows 32 g .. 32 g + 31 of every block. Loads are
+  // unconditional (block index and rows clamped) so the compiler can count outstanding loads exactly; rows at or
+  // beyond L are zeroed when stored (their keys are masked, and their values must not turn 0 * garbage into NaN).
+  constexpr int HK = BK / 2;                       // rows staged per group
+  constexpr int GT = C::NT / 2;                    // threads per group
+  constexpr int KPT = (HK * C::NP + GT - 1) / GT;  // K pieces per thread
+  constexpr int VPT = (HK * C::VP + GT - 1) / GT;  // V pieces per thread
+  const int gt = tid & (GT - 1), row0 = grp * HK;
+  i32x4 kr[KPT];
+  u32x4 vr[VPT];
   float ksr = 0.0f;
-  auto gload = [&](int kb) {
+  auto load_k = [&](int blk) {
+    const int kb = blk * BK + row0;
 #pragma unroll
-    for (int i = 0; i < C::KPT; i++) {
-      const int idx = tid + i * C::NT;
-      const int key = idx / C::NP, pc = idx % C::NP;
-      const bool ok = idx < BK * C::NP && kb + key < p.L;
-      kr[i] = ok ? *(const i32x4 *)(Kh + (size_t)(kb + key) * C::RB + pc * 16) : i32x4{0, 0, 0, 0};
+    for (int i = 0; i < KPT; i++) {
+      const int idx = gt + i * GT;
+      const int key = (idx / C::NP) & (HK - 1), pc = idx % C::NP;
+      kr[i] = *(const i32x4 *)(Kh + (size_t)min(kb + key, Lm1) * C::RB + pc * 16);
     }
-#pragma unroll
-    for (int i = 0; i < C::VPT; i++) {
-      const int task = tid + i * C::NT;
-      const int kg = task % (BK / 4), dg = task / (BK / 4);
-#pragma unroll
-      for (int r = 0; r < 4; r++) {
-        const int key = kb + 4 * kg + r;
-        const bool ok = task < C::NVT && key < p.L;
-        vr[i][r] = ok ? *(const u32x4 *)(Vh + (size_t)key * D * 2 + dg * 16) : u32x4{0, 0, 0, 0};
-      }
-    }
-    if constexpr (C::QK8) ksr = (tid < BK && kb + tid < p.L) ? ksh[kb + tid] : 0.0f;
+    if constexpr (C::QK8) ksr = ksh[min(kb + (gt & (HK - 1)), Lm1)];
   };
-  auto lstore = [&](char *buf) {
+  auto load_v = [&](int blk) {
+    const int kb = blk * BK + row0;
 #pragma unroll
-    for (int i = 0; i < C::KPT; i++) {
-      const int idx = tid + i * C::NT;
-      const int key = idx / C::NP, pc = idx % C::NP;
-      if (idx < BK * C::NP) *(i32x4 *)(buf + key * C::RB + ((pc ^ kswz<C::NP>(key)) * 16)) = kr[i];
+    for (int i = 0; i < VPT; i++) {
+      const int idx = gt + i * GT;
+      const int key = (idx / C::VP) & (HK - 1), pc = idx % C::VP;
+      vr[i] = *(const u32x4 *)(Vh + (size_t)min(kb + key, Lm1) * D * 2 + pc * 16);
     }
-    char *vt = buf + C::KBYTES;
+  };
+  auto store_k = [&](int blk) {
+    char *kbuf = smem + C::KOFF + (blk & 1) * C::KBYTES;
 #pragma unroll
-    for (int i = 0; i < C::VPT; i++) {
-      const int task = tid + i * C::NT;
-      if (task < C::NVT) {
-        const int kg = task % (BK / 4), dg = task / (BK / 4);
-#pragma unroll
-        for (int j = 0; j < 8; j++) {
-          const int d = dg * 8 + j, sh = (j & 1) * 16;
-          const unsigned e0 = (vr[i][0][j >> 1] >> sh) & 0xffffu, e1 = (vr[i][1][j >> 1] >> sh) & 0xffffu;
-          const unsigned e2 = (vr[i][2][j >> 1] >> sh) & 0xffffu, e3 = (vr[i][3][j >> 1] >> sh) & 0xffffu;
-          *(u32x2 *)(vt + d * (BK * 2) + (((kg >> 1) ^ (d & 7)) * 16) + (kg & 1) * 8) =
-              u32x2{e0 | (e1 << 16), e2 | (e3 << 16)};
-        }
-      }
+    for (int i = 0; i < KPT; i++) {
+      const int idx = gt + i * GT;
+      const int key = row0 + idx / C::NP, pc = idx % C::NP;
+      if (idx < HK * C::NP) *(i32x4 *)(kbuf + key * C::RB + ((pc ^ kswz<C::NP>(key)) * 16)) = kr[i];
     }
     if constexpr (C::QK8) {
-      if (tid < BK) ((float *)(vt + C::VBYTES))[tid] = ksr;
+      if (gt < HK)
+        ((float *)(smem + C::SOFF))[(blk % 3) * BK + row0 + gt] = blk * BK + row0 + gt <= Lm1 ? ksr : 0.0f;
+    }
+  };
+  auto store_v = [&](int blk) {
+    char *vbuf = smem + C::VOFF + (blk & 1) * C::VBYTES;
+#pragma unroll
+    for (int i = 0; i < VPT; i++) {
+      const int idx = gt + i * GT;
+      const int key = row0 + idx / C::VP, pc = idx % C::VP;
+      if (idx < HK * C::VP)
+        *(u32x4 *)(vbuf + voff<D>(key, pc)) = blk * BK + key <= Lm1 ? vr[i] : u32x4{0, 0, 0, 0};
     }
   };
 
@@ -221,39 +262,64 @@ void attention_kernel(const char *__restrict__ Q, const char *__restrict__ K, co
 #pragma unroll
     for (int i = 0; i < 16; i++) o[db][i] = 0.0f;
   float m = -INFINITY, l = 0.0f;
+  SAcc s[2];
+  VT8 pb[2][2];
+#pragma unroll
+  for (int t = 0; t < 2; t++)
+#pragma unroll
+    for (int i = 0; i < 16; i++) {
+      s[t][i] = 0;
+      pb[t][i >> 3][i & 7] = (VE)0.0f;
+    }
 
   // K row this lane feeds to the score MFMA of a 32-key tile (before the tile offset)
   const int krow = 16 * (l32 >> 4) + 8 * ((l32 >> 2) & 1) + 4 * ((l32 >> 3) & 1) + (l32 & 3);
+  // transposing V read: this lane's source row and byte offset within a 16-lane group
+  const int l16 = lane & 15;
+  const int tr_row = l16 >> 2, tr_col = (l16 & 3) * 8;
 
-  if (kend > 0) {
-    gload(0);
-    lstore(smem);
-  }
-  __syncthreads();
-  int cur = 0;
-  for (int kb = 0; kb < kend; kb += BK) {
-    const bool more = kb + BK < kend;
-    if (more) gload(kb + BK);
-    const char *Ks = smem + cur * C::BUF;
-    const char *Vt = Ks + C::KBYTES;
-    const float *ksc = (const float *)(Vt + C::VBYTES);
-
-    // S^T tiles for keys kb + 32 t + (0..31)
-    SAcc s[2];
+  // matrix phase of block j: S(j) = K(j) Q^T, then O^T += V(j-1)^T P(j-1)^T
+  auto matrix_phase = [&](int j) {
+    if (j < nblk) {
+      const char *Ks = smem + C::KOFF + (j & 1) * C::KBYTES;
 #pragma unroll
-    for (int t = 0; t < 2; t++) {
+      for (int t = 0; t < 2; t++) {
 #pragma unroll
-      for (int i = 0; i < 16; i++) s[t][i] = 0;
-      const int key = 32 * t + krow;
-      const char *kp = Ks + key * C::RB;
-      const int sw = kswz<C::NP>(key);
+        for (int i = 0; i < 16; i++) s[t][i] = 0;
+        const int key = 32 * t + krow;
+        const char *kp = Ks + key * C::RB;
+        const int sw = kswz<C::NP>(key);
 #pragma unroll
-      for (int c = 0; c < C::NCH; c++) {
-        const i32x4 a = *(const i32x4 *)(kp + (((2 * c + hl) ^ sw) * 16));
-        s[t] = mma_qk<QKT>(a, qreg[c], s[t]);
+        for (int c = 0; c < C::NCH; c++) {
+          const i32x4 a = *(const i32x4 *)(kp + (((2 * c + hl) ^ sw) * 16));
+          s[t] = mma_qk<QKT>(a, qreg[c], s[t]);
+        }
       }
     }
+    if (!DUMP && j >= 1) {
+      const char *Vs = smem + C::VOFF + ((j - 1) & 1) * C::VBYTES;
+#pragma unroll
+      for (int t = 0; t < 2; t++)
+#pragma unroll
+        for (int s2 = 0; s2 < 2; s2++) {
+          // keys 32 t + 16 s2 + 8 hl + (0..3) and (4..7)
+          const int k0 = 32 * t + 16 * s2 + 8 * hl + tr_row;
+#pragma unroll
+          for (int db = 0; db < D / 32; db++) {
+            const int pc = (db * 32 + (l32 & 16)) / 8;  // 16-byte piece holding channel D0
+            const i16x4 lo = lds_tr16(Vs + voff<D>(k0, pc) + tr_col);
+            const i16x4 hi = lds_tr16(Vs + voff<D>(k0 + 4, pc) + tr_col);
+            const i16x8 a = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+            o[db] = mma_pv<VT>(a, pb[t][s2], o[db]);
+          }
+        }
+    }
+  };
 
+  // vector phase of block j: online softmax of S(j) into P(j)
+  auto vector_phase = [&](int j) {
+    if (j < 0 || j >= nblk) return;
+    const int kb = j * BK;
     if constexpr (DUMP) {
       // element i of lane-half hl holds key kb + 32 t + 16 (i / 8) + 8 hl + i % 8
       if (qvalid) {
@@ -269,82 +335,99 @@ void attention_kernel(const char *__restrict__ Q, const char *__restrict__ K, co
             }
           }
       }
-    } else {
-      float x[2][16];
-#pragma unroll
-      for (int t = 0; t < 2; t++) {
-        if constexpr (C::QK8) {
-#pragma unroll
-          for (int s8 = 0; s8 < 2; s8++) {
-            const f32x4 k0 = *(const f32x4 *)(ksc + 32 * t + 16 * s8 + 8 * hl);
-            const f32x4 k1 = *(const f32x4 *)(ksc + 32 * t + 16 * s8 + 8 * hl + 4);
-#pragma unroll
-            for (int j = 0; j < 4; j++) {
-              x[t][8 * s8 + j] = (float)s[t][8 * s8 + j] * k0[j];
-              x[t][8 * s8 + 4 + j] = (float)s[t][8 * s8 + 4 + j] * k1[j];
-            }
-          }
-        } else {
-#pragma unroll
-          for (int i = 0; i < 16; i++) x[t][i] = s[t][i];
-        }
-      }
-      if (CAUSAL || kb + BK > p.L) {
-#pragma unroll
-        for (int t = 0; t < 2; t++)
-#pragma unroll
-          for (int i = 0; i < 16; i++) {
-            const int key = kb + 32 * t + 16 * (i >> 3) + 8 * hl + (i & 7);
-            bool masked = key >= p.L;
-            if constexpr (CAUSAL) masked = masked || key > q + p.causal_off;
-            if (masked) x[t][i] = -INFINITY;
-          }
-      }
-      float amax = -INFINITY;
+      return;
+    }
+    float x[2][16];
+    if constexpr (C::QK8) {
+      const float *ksc = (const float *)(smem + C::SOFF) + (j % 3) * BK;
 #pragma unroll
       for (int t = 0; t < 2; t++)
 #pragma unroll
-        for (int i = 0; i < 16; i++) amax = fmaxf(amax, x[t][i]);
-      // lazy running maximum (wave-uniform branch); partner lanes always update together
-      if (__any(amax * qsc > m + SLACK)) {
-        const float ap = fmaxf(amax, __shfl_xor(amax, 32));
-        const float mn = fmaxf(m, ap * qsc);
-        const float f = mn == -INFINITY ? 1.0f : __builtin_amdgcn_exp2f(m - mn);
-        m = mn;
-        l *= f;
+        for (int s8 = 0; s8 < 2; s8++) {
+          const f32x4 k0 = *(const f32x4 *)(ksc + 32 * t + 16 * s8 + 8 * hl);
+          const f32x4 k1 = *(const f32x4 *)(ksc + 32 * t + 16 * s8 + 8 * hl + 4);
 #pragma unroll
-        for (int db = 0; db < D / 32; db++)
+          for (int e = 0; e < 4; e++) {
+            x[t][8 * s8 + e] = (float)s[t][8 * s8 + e] * k0[e];
+            x[t][8 * s8 + 4 + e] = (float)s[t][8 * s8 + 4 + e] * k1[e];
+          }
+        }
+    } else {
 #pragma unroll
-          for (int i = 0; i < 16; i++) o[db][i] *= f;
-      }
-      const float nm = m == -INFINITY ? 0.0f : -m;
-      VT8 pb[2][2];
+      for (int t = 0; t < 2; t++)
+#pragma unroll
+        for (int i = 0; i < 16; i++) x[t][i] = s[t][i];
+    }
+    if (CAUSAL || kb + BK > p.L) {
 #pragma unroll
       for (int t = 0; t < 2; t++)
 #pragma unroll
         for (int i = 0; i < 16; i++) {
-          const float pv = __builtin_amdgcn_exp2f(fmaf(x[t][i], qsc, nm));
-          l += pv;
-          pb[t][i >> 3][i & 7] = (VE)pv;
-        }
-      // O^T += V^T P^T, 16 keys per MFMA
-#pragma unroll
-      for (int t = 0; t < 2; t++)
-#pragma unroll
-        for (int s2 = 0; s2 < 2; s2++) {
-          const int kp = 4 * t + 2 * s2 + hl;
-#pragma unroll
-          for (int db = 0; db < D / 32; db++) {
-            const int d = db * 32 + l32;
-            const VT8 a = *(const VT8 *)(Vt + d * (BK * 2) + ((kp ^ (d & 7)) * 16));
-            o[db] = mma_pv<VT>(a, pb[t][s2], o[db]);
-          }
+          const int key = kb + 32 * t + 16 * (i >> 3) + 8 * hl + (i & 7);
+          bool masked = key >= p.L;
+          if constexpr (CAUSAL) masked = masked || key > q + p.causal_off;
+          if (masked) x[t][i] = -INFINITY;
         }
     }
-    if (more) lstore(smem + (cur ^ 1) * C::BUF);
-    __syncthreads();
-    cur ^= 1;
+    float amax = -INFINITY;
+#pragma unroll
+    for (int t = 0; t < 2; t++)
+#pragma unroll
+      for (int i = 0; i < 16; i++) amax = fmaxf(amax, x[t][i]);
+    // lazy running maximum (wave-uniform branch); partner lanes always update together
+    if (__any(amax * qsc > m + SLACK)) {
+      const float ap = fmaxf(amax, __shfl_xor(amax, 32));
+      const float mn = fmaxf(m, ap * qsc);
+      const float f = mn == -INFINITY ? 1.0f : __builtin_amdgcn_exp2f(m - mn);
+      m = mn;
+      l *= f;
+#pragma unroll
+      for (int db = 0; db < D / 32; db++)
+#pragma unroll
+        for (int i = 0; i < 16; i++) o[db][i] *= f;
+    }
+    const float nm = m == -INFINITY ? 0.0f : -m;
+#pragma unroll
+    for (int t = 0; t < 2; t++)
+#pragma unroll
+      for (int i = 0; i < 16; i += 2) {
+        const float p0 = __builtin_amdgcn_exp2f(fmaf(x[t][i], qsc, nm));
+        const float p1 = __builtin_amdgcn_exp2f(fmaf(x[t][i + 1], qsc, nm));
+        const VP2 pr = {(VE)p0, (VE)p1};
+        pb[t][i >> 3][i & 7] = pr[0];
+        pb[t][i >> 3][(i & 7) + 1] = pr[1];
+        l = sum2<VT>(pr, l);  // the row sum of the rounded P that P V uses
+      }
+  };
+
+  // Ping-pong schedule. Both groups run the same loop body [matrix(j); stage; barrier; vector(j); barrier],
+  // group 1 entering it one barrier later, so that in every half-step one group is in its matrix phase and the
+  // other in its vector phase (s_barrier counts wave arrivals, not code locations: both groups execute the same
+  // number of barriers). Half-step 2j + g is group g's matrix(j); K(j), V(j-1) are read in half-steps 2j, 2j+1.
+  // Each group stores its half of K(j+1) and V(j) right after its matrix(j) (half-step 2j + g, after every read
+  // of the ring slots they replace) from registers loaded one iteration earlier. Key scales use a 3-deep ring:
+  // scale block j is read by group 1 in half-step 2j + 2.
+  if (nblk > 0) {
+    load_k(0);
+    store_k(0);
+    load_k(min(1, nblk - 1));
+    load_v(0);
   }
+  __syncthreads();
+  if (grp == 1) __syncthreads();
+  for (int j = 0; j <= nblk; j++) {
+    matrix_phase(j);
+    if (j + 1 < nblk) store_k(j + 1);
+    if (j < nblk) store_v(j);
+    __syncthreads();
+    if (j + 1 < nblk) {
+      load_k(min(j + 2, nblk - 1));
+      load_v(j + 1);
+    }
+    vector_phase(j);
+    __syncthreads();
+  }
+  if (grp == 0) __syncthreads();
   if constexpr (!DUMP) {
     const float lt = l + __shfl_xor(l, 32);
     const float inv = lt > 0.0f ? 1.0f / lt : 0.0f;
@@ -364,8 +447,6 @@ void attention_kernel(const char *__restrict__ Q, const char *__restrict__ K, co
   }
 }
 
-constexpr int NW_DEFAULT = 4;
-
 int esize(int t) { return t == T_I8 ? 1 : t == T_F32 ? 4 : 2; }
 
 // Host side: validation (every access the kernel makes must fall inside the
@@ -373,8 +454,7 @@ int esize(int t) { return t == T_I8 ? 1 : t == T_F32 ? 4 : 2; }
 template <int D, int QKT, int VT, int OT, bool CAUSAL, bool DUMP>
 int launch_attention(const Pipeline &pl, hipStream_t stream, const Arg *args, int nargs, const void *params,
                      uint32_t params_len, std::string *err) {
-  constexpr int NW = NW_DEFAULT;
-  using C = Cfg<D, QKT, VT, NW>;
+  using C = Cfg<D, QKT>;
   if (params_len != sizeof(AttnParams)) {
     *err = "parameter block of " + std::to_string(params_len) + " bytes, expected " +
            std::to_string(sizeof(AttnParams));
@@ -445,7 +525,7 @@ int launch_attention(const Pipeline &pl, hipStream_t stream, const Arg *args, in
     *err = "grid too large";
     return -1;
   }
-  auto kern = attention_kernel<D, QKT, VT, OT, CAUSAL, NW, DUMP>;
+  auto kern = attention_kernel<D, QKT, VT, OT, CAUSAL, DUMP>;
   static bool attr_set = false;
   if (!attr_set) {
     hipError_t e = hipFuncSetAttribute((const void *)kern, hipFuncAttributeMaxDynamicSharedMemorySize, C::LDS);
@@ -536,7 +616,7 @@ bool make_attention(const std::string &fn, const Macros &m, Pipeline *pl, std::s
   if (hd == 128) f = dump ? pick_types<128, true>(qkt, it, ot, causal) : pick_types<128, false>(qkt, it, ot, causal);
   else f = dump ? pick_types<64, true>(qkt, it, ot, causal) : pick_types<64, false>(qkt, it, ot, causal);
   pl->launch = f;
-  pl->threads = NW_DEFAULT * 64;
+  pl->threads = NW * 64;
   return true;
 }
 
