@@ -110,17 +110,24 @@ __device__ __forceinline__ i16x4 lds_tr16(const char *p) {
   return __builtin_amdgcn_ds_read_tr16_b64_v4i16((LP)p);
 }
 
-// Swizzle of the 16-byte pieces of a K row in LDS: distinct for the 8 lanes
-// that read one LDS pass (keys differing in bits 0, 1 and 3).
-template <int NP>
+// LDS on gfx950 serves a 16-byte read 16 lanes at a time from 64 four-byte banks (256 bytes per pass).
+// K rows (RB bytes, NP 16-byte pieces) are read 16 lanes = 16 distinct rows at a time: piece p of row `key`
+// is stored at p ^ ((key / (256 / RB)) % NP), so the 16 rows of a pass occupy distinct (bank half, piece)
+// slots. (For 128-byte rows: 2 rows per 256 bytes and 8 pieces each; for 256-byte rows: 16 pieces.)
+template <int RB, int NP>
 __device__ __forceinline__ int kswz(int key) {
-  return ((key & 3) | ((key >> 1) & 4)) & (NP - 1);
+  return (key / (256 / RB)) % NP;
 }
 
-// Byte offset of 16-byte piece pc of V row `key` (32-byte units XOR key % 4).
+// Byte offset of 16-byte piece pc of V row `key` (rows of D bf16/f16). A transposing read covers 4 rows x 32
+// bytes per 16-lane group, two groups (channels D0 and D0 + 16) per pass: 32-byte unit u of the row is stored at
+// u ^ 2 ((key % 4) / R), R = rows per 256 bytes, which puts the two groups in disjoint bank halves and the
+// four rows of each group in distinct banks.
 template <int D>
 __device__ __forceinline__ int voff(int key, int pc) {
-  return key * (D * 2) + ((((pc >> 1) ^ key) & 3) | ((pc >> 1) & ~3)) * 32 + (pc & 1) * 16;
+  constexpr int R = 256 / (D * 2) > 0 ? 256 / (D * 2) : 1;
+  const int u = (pc >> 1) ^ (2 * ((key & 3) / R));
+  return key * (D * 2) + u * 32 + (pc & 1) * 16;
 }
 
 template <int OT>
@@ -151,9 +158,18 @@ struct Cfg {
   static constexpr int KOFF = 0;                          // K ring: 2 blocks
   static constexpr int VOFF = 2 * KBYTES;                 // V ring: 2 blocks
   static constexpr int SOFF = VOFF + 2 * VBYTES;          // key-scale ring: 3 blocks
-  static constexpr int LDS = SOFF + (QK8 ? 3 * BK * 4 : 0);
+  static constexpr int NOFF = SOFF + 3 * BK * 4;          // -C * key-scale ring: 3 blocks
+  static constexpr int LDS = QK8 ? NOFF + 3 * BK * 4 : SOFF;
   static_assert(D % 32 == 0 && D <= 128, "head dim");
 };
+
+// int8 scores: the int32 accumulators start at MAGIC, the bit pattern of the float 1.5 * 2^23. Adding a score
+// s (|s| <= 128 * 127^2 < 2^22) keeps the sum in the binade [2^23, 2^24), where the float with those bits is
+// exactly 1.5 * 2^23 + s. So s * ks = fma(float_bits(acc), ks, -1.5 * 2^23 * ks), one full-rate instruction
+// instead of a half-rate int->float conversion and a multiply (the rounding of -1.5 * 2^23 * ks moves the score
+// by at most 0.75 integer units; the int32 accumulator itself stays exact).
+constexpr int MAGIC = 0x4B400000;
+constexpr float MAGICF = 12582912.0f;
 
 // DUMP: instead of attention, write the raw score accumulators S[h][q][key]
 // (int32 for int8 inputs, fp32 otherwise) of the same MFMA path, for tests.
@@ -200,36 +216,40 @@ __global__ __launch_bounds__(NW * 64) void attention_kernel(const char *__restri
   int kend = p.L;
   if constexpr (CAUSAL) kend = min(p.L, qb * C::BQ + C::BQ + p.causal_off);
   const int nblk = kend > 0 ? (kend + BK - 1) / BK : 0;
-  const int Lm1 = p.L - 1;
 
-  // -- staging: global -> registers -> LDS. Group g stages rows 32 g .. 32 g + 31 of every block. Loads are
-  // unconditional (block index and rows clamped) so the compiler can count outstanding loads exactly; rows at or
-  // beyond L are zeroed when stored (their keys are masked, and their values must not turn 0 * garbage into NaN).
+  // -- staging: global -> registers -> LDS. Group g stages rows 32 g .. 32 g + 31 of every block. Buffer loads
+  // with a per-block descriptor whose range ends at key L: rows at or beyond L read as zero (their keys are
+  // masked, and their values must not turn 0 * garbage into NaN) and nothing past L is ever read. Offsets within
+  // a block are per-thread constants; the descriptor's base advances in scalar registers.
   constexpr int HK = BK / 2;                       // rows staged per group
   constexpr int GT = C::NT / 2;                    // threads per group
   constexpr int KPT = (HK * C::NP + GT - 1) / GT;  // K pieces per thread
   constexpr int VPT = (HK * C::VP + GT - 1) / GT;  // V pieces per thread
   const int gt = tid & (GT - 1), row0 = grp * HK;
   i32x4 kr[KPT];
-  u32x4 vr[VPT];
+  i32x4 vr[VPT];
   float ksr = 0.0f;
+  auto rsrc = [&](const void *base, int blk, int row_bytes) {
+    const int rows = max(0, p.L - blk * BK);
+    return __builtin_amdgcn_make_buffer_rsrc((void *)((const char *)base + (size_t)blk * BK * row_bytes), (short)0,
+                                             rows * row_bytes, 0x00020000);
+  };
   auto load_k = [&](int blk) {
-    const int kb = blk * BK + row0;
+    const __amdgpu_buffer_rsrc_t r = rsrc(Kh, blk, C::RB);
 #pragma unroll
     for (int i = 0; i < KPT; i++) {
-      const int idx = gt + i * GT;
-      const int key = (idx / C::NP) & (HK - 1), pc = idx % C::NP;
-      kr[i] = *(const i32x4 *)(Kh + (size_t)min(kb + key, Lm1) * C::RB + pc * 16);
+      const int idx = (gt + i * GT) % (HK * C::NP);
+      kr[i] = __builtin_amdgcn_raw_buffer_load_b128(r, (row0 + idx / C::NP) * C::RB + (idx % C::NP) * 16, 0, 0);
     }
-    if constexpr (C::QK8) ksr = ksh[min(kb + (gt & (HK - 1)), Lm1)];
+    if constexpr (C::QK8)
+      ksr = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rsrc(ksh, blk, 4), (row0 + (gt & (HK - 1))) * 4, 0, 0));
   };
   auto load_v = [&](int blk) {
-    const int kb = blk * BK + row0;
+    const __amdgpu_buffer_rsrc_t r = rsrc(Vh, blk, D * 2);
 #pragma unroll
     for (int i = 0; i < VPT; i++) {
-      const int idx = gt + i * GT;
-      const int key = (idx / C::VP) & (HK - 1), pc = idx % C::VP;
-      vr[i] = *(const u32x4 *)(Vh + (size_t)min(kb + key, Lm1) * D * 2 + pc * 16);
+      const int idx = (gt + i * GT) % (HK * C::VP);
+      vr[i] = __builtin_amdgcn_raw_buffer_load_b128(r, (row0 + idx / C::VP) * D * 2 + (idx % C::VP) * 16, 0, 0);
     }
   };
   auto store_k = [&](int blk) {
@@ -238,11 +258,13 @@ __global__ __launch_bounds__(NW * 64) void attention_kernel(const char *__restri
     for (int i = 0; i < KPT; i++) {
       const int idx = gt + i * GT;
       const int key = row0 + idx / C::NP, pc = idx % C::NP;
-      if (idx < HK * C::NP) *(i32x4 *)(kbuf + key * C::RB + ((pc ^ kswz<C::NP>(key)) * 16)) = kr[i];
+      if (idx < HK * C::NP) *(i32x4 *)(kbuf + key * C::RB + ((pc ^ kswz<C::RB, C::NP>(key)) * 16)) = kr[i];
     }
     if constexpr (C::QK8) {
-      if (gt < HK)
-        ((float *)(smem + C::SOFF))[(blk % 3) * BK + row0 + gt] = blk * BK + row0 + gt <= Lm1 ? ksr : 0.0f;
+      if (gt < HK) {
+        ((float *)(smem + C::SOFF))[(blk % 3) * BK + row0 + gt] = ksr;
+        ((float *)(smem + C::NOFF))[(blk % 3) * BK + row0 + gt] = -MAGICF * ksr;
+      }
     }
   };
   auto store_v = [&](int blk) {
@@ -251,8 +273,7 @@ __global__ __launch_bounds__(NW * 64) void attention_kernel(const char *__restri
     for (int i = 0; i < VPT; i++) {
       const int idx = gt + i * GT;
       const int key = row0 + idx / C::VP, pc = idx % C::VP;
-      if (idx < HK * C::VP)
-        *(u32x4 *)(vbuf + voff<D>(key, pc)) = blk * BK + key <= Lm1 ? vr[i] : u32x4{0, 0, 0, 0};
+      if (idx < HK * C::VP) *(i32x4 *)(vbuf + voff<D>(key, pc)) = vr[i];
     }
   };
 
@@ -264,6 +285,9 @@ __global__ __launch_bounds__(NW * 64) void attention_kernel(const char *__restri
   float m = -INFINITY, l = 0.0f;
   SAcc s[2];
   VT8 pb[2][2];
+  SAcc sinit;
+#pragma unroll
+  for (int i = 0; i < 16; i++) sinit[i] = C::QK8 ? MAGIC : 0;
 #pragma unroll
   for (int t = 0; t < 2; t++)
 #pragma unroll
@@ -280,78 +304,105 @@ __global__ __launch_bounds__(NW * 64) void attention_kernel(const char *__restri
 
   // matrix phase of block j: S(j) = K(j) Q^T, then O^T += V(j-1)^T P(j-1)^T
   auto matrix_phase = [&](int j) {
+    // Operands are fetched ahead of the MFMAs that consume them (LDS latency is long while the other waves
+    // stream their own operands): all K operands first, then the V operands of each 16-key step of P V one step
+    // ahead (double-buffered).
+    const char *Vs = smem + C::VOFF + ((j - 1) & 1) * C::VBYTES;
+    auto vload = [&](int st, i16x8 (&va)[D / 32]) {
+      const int t = st >> 1, s2 = st & 1;
+      const int k0 = 32 * t + 16 * s2 + 8 * hl + tr_row;  // keys k0 .. k0+3 and k0+4 .. k0+7 of the step
+#pragma unroll
+      for (int db = 0; db < D / 32; db++) {
+        const int pc = (db * 32 + (l32 & 16)) / 8;  // 16-byte piece holding channel D0
+        const i16x4 lo = lds_tr16(Vs + voff<D>(k0, pc) + tr_col);
+        const i16x4 hi = lds_tr16(Vs + voff<D>(k0 + 4, pc) + tr_col);
+        va[db] = i16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+      }
+    };
+    const bool do_pv = !DUMP && j >= 1;
+    i16x8 va[2][D / 32];
     if (j < nblk) {
       const char *Ks = smem + C::KOFF + (j & 1) * C::KBYTES;
+      i32x4 ka[2][C::NCH];
 #pragma unroll
       for (int t = 0; t < 2; t++) {
-#pragma unroll
-        for (int i = 0; i < 16; i++) s[t][i] = 0;
         const int key = 32 * t + krow;
         const char *kp = Ks + key * C::RB;
-        const int sw = kswz<C::NP>(key);
+        const int sw = kswz<C::RB, C::NP>(key);
 #pragma unroll
-        for (int c = 0; c < C::NCH; c++) {
-          const i32x4 a = *(const i32x4 *)(kp + (((2 * c + hl) ^ sw) * 16));
-          s[t] = mma_qk<QKT>(a, qreg[c], s[t]);
-        }
+        for (int c = 0; c < C::NCH; c++) ka[t][c] = *(const i32x4 *)(kp + (((2 * c + hl) ^ sw) * 16));
       }
-    }
-    if (!DUMP && j >= 1) {
-      const char *Vs = smem + C::VOFF + ((j - 1) & 1) * C::VBYTES;
+      if (do_pv) vload(0, va[0]);
 #pragma unroll
       for (int t = 0; t < 2; t++)
 #pragma unroll
-        for (int s2 = 0; s2 < 2; s2++) {
-          // keys 32 t + 16 s2 + 8 hl + (0..3) and (4..7)
-          const int k0 = 32 * t + 16 * s2 + 8 * hl + tr_row;
+        for (int c = 0; c < C::NCH; c++) s[t] = mma_qk<QKT>(ka[t][c], qreg[c], c == 0 ? sinit : s[t]);
+    } else if (do_pv) {
+      vload(0, va[0]);
+    }
+    if (do_pv) {
 #pragma unroll
-          for (int db = 0; db < D / 32; db++) {
-            const int pc = (db * 32 + (l32 & 16)) / 8;  // 16-byte piece holding channel D0
-            const i16x4 lo = lds_tr16(Vs + voff<D>(k0, pc) + tr_col);
-            const i16x4 hi = lds_tr16(Vs + voff<D>(k0 + 4, pc) + tr_col);
-            const i16x8 a = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-            o[db] = mma_pv<VT>(a, pb[t][s2], o[db]);
-          }
-        }
+      for (int st = 0; st < 4; st++) {
+        if (st < 3) vload(st + 1, va[(st + 1) & 1]);
+#pragma unroll
+        for (int db = 0; db < D / 32; db++) o[db] = mma_pv<VT>(va[st & 1][db], pb[st >> 1][st & 1], o[db]);
+      }
     }
   };
 
-  // vector phase of block j: online softmax of S(j) into P(j)
+  // vector phase of block j: the scores in log2 units (x, masked keys at -inf), the lazy rescale, then
+  // P(j) = 2^(x qsc - m) and the row sums
   auto vector_phase = [&](int j) {
     if (j < 0 || j >= nblk) return;
-    const int kb = j * BK;
     if constexpr (DUMP) {
-      // element i of lane-half hl holds key kb + 32 t + 16 (i / 8) + 8 hl + i % 8
+      // element i of lane-half hl holds key 64 j + 32 t + 16 (i / 8) + 8 hl + i % 8
       if (qvalid) {
 #pragma unroll
         for (int t = 0; t < 2; t++)
 #pragma unroll
           for (int i = 0; i < 16; i++) {
-            const int key = kb + 32 * t + 16 * (i >> 3) + 8 * hl + (i & 7);
+            const int key = j * BK + 32 * t + 16 * (i >> 3) + 8 * hl + (i & 7);
             if (key < p.L) {
               float *dst = (float *)O + ((size_t)h * p.Lq + q) * p.L + key;
-              if constexpr (C::QK8) *(int *)dst = s[t][i];
+              if constexpr (C::QK8) *(int *)dst = s[t][i] - MAGIC;
               else *dst = s[t][i];
             }
           }
       }
       return;
     }
+    const int kb = j * BK;
     float x[2][16];
+    // element i of lane-half hl holds key kb + 32 t + 16 (i / 8) + 8 hl + i % 8
     if constexpr (C::QK8) {
       const float *ksc = (const float *)(smem + C::SOFF) + (j % 3) * BK;
+      const float *nbc = (const float *)(smem + C::NOFF) + (j % 3) * BK;
+      // all key scales of the block first: one LDS round trip instead of one per group of four keys
+      f32x4 k4[2][2][2], n4[2][2][2];
 #pragma unroll
       for (int t = 0; t < 2; t++)
 #pragma unroll
-        for (int s8 = 0; s8 < 2; s8++) {
-          const f32x4 k0 = *(const f32x4 *)(ksc + 32 * t + 16 * s8 + 8 * hl);
-          const f32x4 k1 = *(const f32x4 *)(ksc + 32 * t + 16 * s8 + 8 * hl + 4);
+        for (int s8 = 0; s8 < 2; s8++)
 #pragma unroll
-          for (int e = 0; e < 4; e++) {
-            x[t][8 * s8 + e] = (float)s[t][8 * s8 + e] * k0[e];
-            x[t][8 * s8 + 4 + e] = (float)s[t][8 * s8 + 4 + e] * k1[e];
+          for (int hh = 0; hh < 2; hh++) {
+            const int off = 32 * t + 16 * s8 + 8 * hl + 4 * hh;
+            k4[t][s8][hh] = *(const f32x4 *)(ksc + off);
+            n4[t][s8][hh] = *(const f32x4 *)(nbc + off);
           }
-        }
+#pragma unroll
+      for (int t = 0; t < 2; t++) {
+        // bit-cast the whole tile (per-element casts of an MFMA result have been miscompiled into a splat)
+        const f32x16 sf = __builtin_bit_cast(f32x16, s[t]);
+#pragma unroll
+        for (int s8 = 0; s8 < 2; s8++)
+#pragma unroll
+          for (int hh = 0; hh < 2; hh++)
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+              const int i = 8 * s8 + 4 * hh + e;
+              x[t][i] = fmaf(sf[i], k4[t][s8][hh][e], n4[t][s8][hh][e]);
+            }
+      }
     } else {
 #pragma unroll
       for (int t = 0; t < 2; t++)
@@ -369,11 +420,12 @@ __global__ __launch_bounds__(NW * 64) void attention_kernel(const char *__restri
           if (masked) x[t][i] = -INFINITY;
         }
     }
-    float amax = -INFINITY;
+    float am[2] = {-INFINITY, -INFINITY};  // two independent chains
 #pragma unroll
     for (int t = 0; t < 2; t++)
 #pragma unroll
-      for (int i = 0; i < 16; i++) amax = fmaxf(amax, x[t][i]);
+      for (int i = 0; i < 16; i++) am[t] = fmaxf(am[t], x[t][i]);
+    const float amax = fmaxf(am[0], am[1]);
     // lazy running maximum (wave-uniform branch); partner lanes always update together
     if (__any(amax * qsc > m + SLACK)) {
       const float ap = fmaxf(amax, __shfl_xor(amax, 32));
@@ -387,6 +439,7 @@ __global__ __launch_bounds__(NW * 64) void attention_kernel(const char *__restri
         for (int i = 0; i < 16; i++) o[db][i] *= f;
     }
     const float nm = m == -INFINITY ? 0.0f : -m;
+    float ls[2] = {0.0f, 0.0f};  // the row sum of the rounded P that P V uses, two independent chains
 #pragma unroll
     for (int t = 0; t < 2; t++)
 #pragma unroll
@@ -396,8 +449,9 @@ __global__ __launch_bounds__(NW * 64) void attention_kernel(const char *__restri
         const VP2 pr = {(VE)p0, (VE)p1};
         pb[t][i >> 3][i & 7] = pr[0];
         pb[t][i >> 3][(i & 7) + 1] = pr[1];
-        l = sum2<VT>(pr, l);  // the row sum of the rounded P that P V uses
+        ls[t] = sum2<VT>(pr, ls[t]);
       }
+    l += ls[0] + ls[1];
   };
 
   // Ping-pong schedule. Both groups run the same loop body [matrix(j); stage; barrier; vector(j); barrier],
@@ -410,7 +464,7 @@ __global__ __launch_bounds__(NW * 64) void attention_kernel(const char *__restri
   if (nblk > 0) {
     load_k(0);
     store_k(0);
-    load_k(min(1, nblk - 1));
+    load_k(1);
     load_v(0);
   }
   __syncthreads();
@@ -420,10 +474,8 @@ __global__ __launch_bounds__(NW * 64) void attention_kernel(const char *__restri
     if (j + 1 < nblk) store_k(j + 1);
     if (j < nblk) store_v(j);
     __syncthreads();
-    if (j + 1 < nblk) {
-      load_k(min(j + 2, nblk - 1));
-      load_v(j + 1);
-    }
+    load_k(j + 2);  // unconditional: blocks past L read as zeros, and the outstanding-load count stays exact
+    load_v(j + 1);
     vector_phase(j);
     __syncthreads();
   }
