@@ -104,6 +104,20 @@ def cpu_baseline(cfg, L, budget_s=20.0):
                       f"extrapolated x{H} heads = {total:.2f} s per call"}
 
 
+def traffic(kernel, cfg="c4"):
+    """HBM bytes per launch of `kernel` at `cfg`, from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE runs
+    (profiles/hbm_traffic_c4.md: the counters scaled by what they read for a plain copy of known size); None for
+    other configs or when the profile is absent."""
+    path = os.path.join(ROOT, "profiles", f"hbm_traffic_{cfg}.json")
+    if not os.path.exists(path) or CONFIGS_ARG.get("config") != cfg:
+        return None
+    with open(path) as f:
+        return int(json.load(f)[kernel]["traffic_bytes"])
+
+
+CONFIGS_ARG = {}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=int(os.environ.get("WORLD_SIZE", "1")))
@@ -112,7 +126,19 @@ def main():
     ap.add_argument("--config", default="c4", choices=sorted(CONFIGS))
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--cpu-budget", type=float, default=20.0)
+    ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
+                    help="only run a plain device copy of MIB MiB (to scale rocprofv3 FETCH_SIZE / WRITE_SIZE)")
     args = ap.parse_args()
+    CONFIGS_ARG["config"] = args.config
+    if args.calibrate_copy:
+        import torch
+        n = args.calibrate_copy * 2 ** 20
+        a = torch.ones(n, dtype=torch.uint8, device="cuda")
+        b = torch.empty_like(a)
+        b.copy_(a)
+        torch.cuda.synchronize()
+        print(json.dumps({"calibrate_copy_bytes": n}))
+        return
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build runs the attention path on a single MI355X (no multi-GPU "
               f"path), so --gpus {args.gpus} is not supported", file=sys.stderr)
@@ -165,7 +191,7 @@ def main():
         "pct_of_peak": round(100 * value * 1e12 / peak, 2),
         "wall_ms_per_step": round(wall_s / args.steps * 1e3, 4),
         "roofline": {"bound": "mfma", "achieved": round(achieved / 1e12, 2), "peak": peak / 1e12,
-                     "unit": "TFLOP/s", "frac": round(achieved / peak, 4), "traffic": None,
+                     "unit": "TFLOP/s", "frac": round(achieved / peak, 4), "traffic": traffic("attention_kernel"),
                      "kernel": "attention_kernel (int8 QK, bf16 PV)" if path == "int8" else "attention_kernel (bf16)",
                      "per_launch_ms": round(per_launch * 1e3, 4)},
     }
@@ -179,7 +205,7 @@ def main():
         # algorithmic bytes: read Q, K, V bf16; write Q, K int8, V bf16, one fp32 scale per Q/K row
         nbytes = S * 3 * H * D * 2 + 2 * S * H * D + S * H * D * 2 + 2 * S * H * 4
         out["prepass"] = {"ms": round(pt * 1e3, 4), "bytes": nbytes, "GB/s": round(nbytes / pt / 1e9, 1),
-                          "frac_hbm": round(nbytes / pt / HBM_PEAK, 4)}
+                          "frac_hbm": round(nbytes / pt / HBM_PEAK, 4), "traffic": traffic("qk_norm_rope_kernel")}
     if not args.no_cpu:
         out["cpu_baseline"] = cpu_baseline(args.config, L, args.cpu_budget)
     gpu.close()

@@ -550,11 +550,10 @@ int launch_attention(const Pipeline &pl, hipStream_t stream, const Arg *args, in
     return true;
   };
   const uint64_t es = esize(QKT);
-  if (!fits(0, (uint64_t)p.H * p.q_rows * D * es, "q") || !fits(1, (uint64_t)p.KVH * p.k_rows * D * es, "k") ||
-      !fits(2, (uint64_t)p.KVH * p.k_rows * D * 2, "v"))
-    return -1;
-  if (qk8 && (!fits(5, (uint64_t)p.H * p.q_rows * 4, "q_scale") || !fits(6, (uint64_t)p.KVH * p.k_rows * 4, "k_scale")))
-    return -1;
+  // extents actually read: rows < Lq of every query head, rows < L of every key/value head
+  const uint64_t qx = (uint64_t)(p.H - 1) * p.q_rows + p.Lq, kx = (uint64_t)(p.KVH - 1) * p.k_rows + p.L;
+  if (!fits(0, qx * D * es, "q") || !fits(1, kx * D * es, "k") || !fits(2, kx * D * 2, "v")) return -1;
+  if (qk8 && (!fits(5, qx * 4, "q_scale") || !fits(6, kx * 4, "k_scale"))) return -1;
   if (DUMP) {
     if (!fits(3, (uint64_t)p.H * p.Lq * p.L * 4, "scores")) return -1;
   } else if (p.Lq > 0) {

@@ -228,7 +228,13 @@ int launch_qk(const Pipeline &pl, hipStream_t stream, const Arg *a, int nargs, c
   };
   const uint64_t nseq = p.M ? (uint64_t)(p.M - 1) / p.seq_len + 1 : 0;
   const uint64_t in_bytes = p.M ? ((uint64_t)(p.M - 1) * p.in_stride + (uint64_t)nslots * HDIM) * esize(IN_T) : 0;
-  const uint64_t hq = nseq * p.Hq * p.out_rows, hk = nseq * p.Hk * p.out_rows, hv = nseq * p.Hv * p.out_rows;
+  // Rows written per output: head-major rows up to (last head) * out_rows + (rows of a sequence). Callers pass
+  // views that start inside a head's row block (h3metal/flux2.py:417-426 writes text rows, then image rows at
+  // offset r0), so the check is on the extent actually touched, not on heads * out_rows.
+  auto extent = [&](int heads) -> uint64_t {
+    return heads && nseq ? (nseq * heads - 1) * (uint64_t)p.out_rows + (uint64_t)rows : 0;
+  };
+  const uint64_t hq = extent(p.Hq), hk = extent(p.Hk), hv = extent(p.Hv);
   const uint64_t tab = (uint64_t)rows * (p.rot / 2) * 4;
   if (!need(0, in_bytes, "qkv", true) || !need(1, HDIM * 4, "wq", p.norm && p.Hq) ||
       !need(2, HDIM * 4, "wk", p.norm && p.Hk) || !need(3, tab, "cos", p.rot > 0 && (p.Hq + p.Hk)) ||

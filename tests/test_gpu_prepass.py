@@ -214,3 +214,35 @@ def test_rotation_reduces_int8_attention_error(gpu):
         errs[qk_rot] = float(np.linalg.norm(got - ref) / np.linalg.norm(ref))
     print("relative errors", errs)
     assert errs[True] < 0.6 * errs[False], errs
+
+
+def test_per_stream_row_offset_views(gpu):
+    """FLUX.2's double-stream blocks (h3metal/flux2.py:417-426) run the pre-pass once per stream, text rows then
+    image rows, each writing into the shared Q/K/V and scale buffers through views offset by r0 rows, with the
+    rotary tables' rows r0 .. r0 + M. Two calls must equal the oracle over all rows."""
+    rng = np.random.default_rng(15)
+    H, hd, T, Mi, rot = 3, 128, 40, 88, 128
+    S = T + Mi
+    Sp = 256
+    x = to_bf16((rng.standard_normal((S, 3 * H * hd)) * 1.5).astype(np.float32))
+    wq, wk = rng.uniform(0.5, 1.5, (2, hd)).astype(np.float32)
+    ang = rng.uniform(0, 6.28, (S, rot // 2))
+    cs, sn = np.cos(ang).astype(np.float32), np.sin(ang).astype(np.float32)
+    Q, K = gpu.empty((H, Sp, hd), "i8"), gpu.empty((H, Sp, hd), "i8")
+    V = gpu.empty((H, Sp, hd), "bf16")
+    qs, ks = gpu.empty((H, Sp), "f32"), gpu.empty((H, Sp), "f32")
+    Wq, Wk, Cs, Sn = gpu.upload(wq), gpu.upload(wk), gpu.upload(cs), gpu.upload(sn)
+    for r0, M in ((0, T), (T, Mi)):  # two streams, separate source tensors
+        src = gpu.upload(x[r0:r0 + M], "bf16")
+        ops.qk_norm_rope(gpu, src, Wq, Wk, Cs.row(r0, M), Sn.row(r0, M), Q.view(Q.shape, offset_elems=r0 * hd),
+                         K.view(K.shape, offset_elems=r0 * hd), V.view(V.shape, offset_elems=r0 * hd), M=M, Hq=H, Hk=H,
+                         Hv=H, hd=hd, out_rows=Sp, rot=rot, eps=1e-6, in_stride=3 * H * hd,
+                         q_scale=qs.view(qs.shape, offset_elems=r0), k_scale=ks.view(ks.shape, offset_elems=r0),
+                         qk_rot=True)
+    gpu.wait()
+    want = op.qk_norm_rope(from_bf16(x), Hq=H, Hk=H, Hv=H, hd=hd, out_rows=Sp, rot=rot, eps=1e-6, norm=True, wq=wq,
+                           wk=wk, cs=cs, sn=sn, q8=True, qk_rot=True)
+    assert np.array_equal(Q.numpy(), want["Q"]) and np.array_equal(K.numpy(), want["K"])
+    assert np.array_equal(qs.numpy().view(np.uint32), want["qs"].view(np.uint32))
+    assert np.array_equal(ks.numpy().view(np.uint32), want["ks"].view(np.uint32))
+    assert np.array_equal(V.numpy(), to_bf16(want["V"]))

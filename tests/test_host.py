@@ -118,3 +118,39 @@ def test_tensor_views():
     assert r.offset == 3 * 4 * 2 and r.shape == (2, 4)
     v = t.view((5, 8), "i8", offset_elems=4)
     assert v.offset == 8 and v.dtype == "i8" and v.nbytes == 40
+
+
+def test_lds_swizzles_cover_all_banks():
+    """The LDS layouts of csrc/attention.hip (kswz, voff), restated: each is a permutation of a row's 16-byte
+    pieces, and every read pass of the score MFMA's K operand (16 lanes of 16 bytes) and of the transposing V
+    read (32 lanes of 8 bytes) touches each of the 64 four-byte banks exactly once."""
+    def kswz(key, RB, NP):
+        return (key // (256 // RB)) % NP
+
+    def voff(key, pc, D):
+        R = max(256 // (D * 2), 1)
+        u = (pc >> 1) ^ (2 * ((key & 3) // R))
+        return key * D * 2 + u * 32 + (pc & 1) * 16
+
+    for D, RB in ((128, 128), (128, 256), (64, 64), (64, 128)):
+        NP, VP = RB // 16, D * 2 // 16
+        for key in range(64):
+            assert sorted(p ^ kswz(key, RB, NP) for p in range(NP)) == list(range(NP))
+            assert sorted(voff(key, pc, D) - key * D * 2 for pc in range(VP)) == [16 * i for i in range(VP)]
+        for c in range(NP // 2):
+            for h in (0, 1):
+                for g in (0, 1):
+                    banks = []
+                    for a in range(16 * g, 16 * g + 16):
+                        key = 16 * (a >> 4) + 8 * ((a >> 2) & 1) + 4 * ((a >> 3) & 1) + (a & 3)
+                        addr = key * RB + (((2 * c + h) ^ kswz(key, RB, NP)) * 16)
+                        banks += [(addr // 4 + i) % 64 for i in range(4)]
+                    assert sorted(banks) == list(range(64))
+        for db in range(D // 32):
+            for h in (0, 1):
+                banks = []
+                for lane in range(32 * h, 32 * h + 32):
+                    l16, l32 = lane & 15, lane & 31
+                    addr = voff(8 * h + (l16 >> 2), (db * 32 + (l32 & 16)) // 8, D) + (l16 & 3) * 8
+                    banks += [(addr // 4 + i) % 64 for i in range(2)]
+                assert sorted(banks) == list(range(64))
