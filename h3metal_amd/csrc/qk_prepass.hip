@@ -24,13 +24,16 @@
 //
 // gfx950 layout: a wave of 64 lanes handles two slots, 32 lanes per slot and
 // HDIM/32 channels per lane (lane l: channels l*PER .. l*PER + PER-1), so every
-// cross-lane step stays inside a half wave; a workgroup of 256 threads handles
-// 8 slots of one row. The kernel is HBM-bound: one read of the row, one write
-// of the codes / halves.
+// cross-lane step stays inside a half wave and runs on DPP / ds_swizzle (no LDS
+// memory traffic). A workgroup of 256 threads covers 8 slots of 8 consecutive
+// rows; each wave issues all 8 rows' loads before processing them, so enough
+// bytes are in flight to stream HBM, and a slot's 8 scales are stored together.
+// The kernel is HBM-bound: one read of the rows, one write of the codes / values.
 #include "h3hip_internal.h"
 
 #include <cmath>
 #include <cstring>
+#include <type_traits>
 
 namespace h3 {
 namespace {
@@ -44,13 +47,26 @@ template <> struct Elem<T_F32> { using type = float; };
 
 template <int N, typename E> struct VecOf { typedef E type __attribute__((ext_vector_type(N))); };
 
-constexpr int SLOTS_PER_WG = 8;
+constexpr int SLOTS_PER_WG = 8;  // (row, head) slots: two per wave, 32 lanes each
+constexpr int RPW = 8;           // rows per workgroup; each wave walks them with all their loads in flight
 
 template <int HDIM>
 constexpr double inv_sqrt_hdim() {
   return HDIM == 128 ? 0.0883883476483184405501055452631 : HDIM == 64 ? 0.125 : 0.1767766952966368811;
 }
 
+// v from lane (lane ^ S) of the same 32-lane half: DPP for S = 1, 2, ds_swizzle (no memory access) for 4, 8, 16.
+template <int S>
+__device__ __forceinline__ float xshfl(float v) {
+  const int x = __builtin_bit_cast(int, v);
+  if constexpr (S == 1) return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, x, 0xB1, 0xF, 0xF, false));
+  else if constexpr (S == 2) return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, x, 0x4E, 0xF, 0xF, false));
+  else return __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(x, 0x1F | (S << 10)));
+}
+
+// Workgroup (bx, by): rows bx*RPW .. bx*RPW + RPW-1, slots by*8 .. by*8 + 7. A half wave owns one slot and
+// walks the rows; lane l32 keeps the scale of row l32 so that a slot's RPW scales (consecutive in memory within
+// a sequence) are stored together after the rows.
 template <int HDIM, int IN_T, int QK_T, int V_T, bool QKROT>
 __global__ __launch_bounds__(256) void qk_norm_rope_kernel(const char *__restrict__ in, const float *__restrict__ wq,
                                                             const float *__restrict__ wk,
@@ -61,111 +77,139 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kernel(const char *__restric
                                                             QkRopeParams p) {
   constexpr int PER = HDIM / 32;
   using IE = typename Elem<IN_T>::type;
+  typedef typename VecOf<PER, IE>::type IV;
   const int lane = threadIdx.x & 63, hl = lane >> 5, l32 = lane & 31, w = threadIdx.x >> 6;
-  const int m = blockIdx.x;
-  const int sq = m / p.seq_len, r = m - sq * p.seq_len;
   const int slot = blockIdx.y * SLOTS_PER_WG + w * 2 + hl;
   const int nslots = p.Hq + p.Hk + p.Hv;
   if (slot >= nslots) return;  // whole half-waves only; no cross-lane step crosses halves
+  const int m0 = blockIdx.x * RPW;
+  const int nr = min(RPW, p.M - m0);
 
-  float v[PER];
+  IV xin[RPW];
   {
-    const IE *src = (const IE *)in + (size_t)m * p.in_stride + (size_t)slot * HDIM + l32 * PER;
-    typedef typename VecOf<PER, IE>::type IV;
-    const IV x = *(const IV *)src;
+    const IE *src = (const IE *)in + (size_t)m0 * p.in_stride + (size_t)slot * HDIM + l32 * PER;
 #pragma unroll
-    for (int i = 0; i < PER; i++) v[i] = (float)x[i];
+    for (int r = 0; r < RPW; r++) xin[r] = *(const IV *)(src + (size_t)min(r, nr - 1) * p.in_stride);
   }
+  const bool isqk = slot < p.Hq + p.Hk, isq = slot < p.Hq;
+  const int h = isq ? slot : isqk ? slot - p.Hq : slot - p.Hq - p.Hk;
+  const int heads = isq ? p.Hq : isqk ? p.Hk : p.Hv;
+  auto hrow_of = [&](int m) {
+    const int sq = m / p.seq_len, r = m - sq * p.seq_len;
+    return ((size_t)sq * heads + h) * p.out_rows + r;
+  };
+  float keep = 1.0f;  // lane l32 < nr: the scale of row m0 + l32
 
-  if (slot < p.Hq + p.Hk) {
-    const bool isq = slot < p.Hq;
-    const int h = isq ? slot : slot - p.Hq;
-    if (p.norm) {
-      float ss = v[0] * v[0];
 #pragma unroll
-      for (int i = 1; i < PER; i++) ss = ss + v[i] * v[i];
+  for (int rr = 0; rr < RPW; rr++) {
+    if (rr >= nr) break;
+    const int m = m0 + rr;
+    float v[PER];
 #pragma unroll
-      for (int s = 16; s >= 1; s >>= 1) ss = ss + __shfl_xor(ss, s);
-      const float inv = 1.0f / sqrtf(ss / (float)HDIM + p.eps);
-      const float *wv = (isq ? wq : wk) + l32 * PER;
+    for (int i = 0; i < PER; i++) v[i] = (float)xin[rr][i];
+    const size_t hrow = hrow_of(m);
+    if (isqk) {
+      if (p.norm) {
+        float ss = v[0] * v[0];
 #pragma unroll
-      for (int i = 0; i < PER; i++) v[i] = (v[i] * inv) * wv[i];
-    }
-    if (p.rot) {
-      const int half_rot = p.rot / 2;
-      const int lanes = half_rot / PER;  // lanes holding the first half of the rotated channels
-      const int src_lane = l32 < lanes ? l32 + lanes : (l32 < 2 * lanes ? l32 - lanes : l32);
-      float pv[PER];
+        for (int i = 1; i < PER; i++) ss = ss + v[i] * v[i];
+        ss = ss + xshfl<16>(ss);
+        ss = ss + xshfl<8>(ss);
+        ss = ss + xshfl<4>(ss);
+        ss = ss + xshfl<2>(ss);
+        ss = ss + xshfl<1>(ss);
+        const float inv = 1.0f / sqrtf(ss / (float)HDIM + p.eps);
+        const float *wv = (isq ? wq : wk) + l32 * PER;
 #pragma unroll
-      for (int i = 0; i < PER; i++) pv[i] = __shfl(v[i], (lane & 32) + src_lane);
-      if (l32 < 2 * lanes) {
-        const bool first = l32 < lanes;
-        const int base = (first ? l32 : l32 - lanes) * PER;  // pair index of v[0]
-        const float *c = cs + (size_t)r * half_rot + base;
-        const float *s = sn + (size_t)r * half_rot + base;
-#pragma unroll
-        for (int i = 0; i < PER; i++) v[i] = first ? v[i] * c[i] - pv[i] * s[i] : v[i] * c[i] + pv[i] * s[i];
+        for (int i = 0; i < PER; i++) v[i] = (v[i] * inv) * wv[i];
       }
-    }
-    if constexpr (QKROT) {
+      if (p.rot) {
+        const int r = m % p.seq_len;
+        const int half_rot = p.rot / 2;
+        const int lanes = half_rot / PER;  // lanes holding the first half of the rotated channels
+        const int src_lane = l32 < lanes ? l32 + lanes : (l32 < 2 * lanes ? l32 - lanes : l32);
+        float pv[PER];
 #pragma unroll
-      for (int i = 0; i < PER; i++) {
-        const unsigned c = (unsigned)(l32 * PER + i);
-        if (__builtin_popcount(c * 0x2545F491u) & 1u) v[i] = -v[i];
+        for (int i = 0; i < PER; i++) pv[i] = __shfl(v[i], (lane & 32) + src_lane);
+        if (l32 < 2 * lanes) {
+          const bool first = l32 < lanes;
+          const int base = (first ? l32 : l32 - lanes) * PER;  // pair index of v[0]
+          const float *c = cs + (size_t)r * half_rot + base;
+          const float *s = sn + (size_t)r * half_rot + base;
+#pragma unroll
+          for (int i = 0; i < PER; i++) v[i] = first ? v[i] * c[i] - pv[i] * s[i] : v[i] * c[i] + pv[i] * s[i];
+        }
       }
-#pragma unroll
-      for (int s = 1; s < PER; s <<= 1) {
+      if constexpr (QKROT) {
 #pragma unroll
         for (int i = 0; i < PER; i++) {
-          if (!(i & s)) {
-            const float a = v[i], b = v[i + s];
-            v[i] = a + b;
-            v[i + s] = a - b;
+          const unsigned c = (unsigned)(l32 * PER + i);
+          if (__builtin_popcount(c * 0x2545F491u) & 1u) v[i] = -v[i];
+        }
+#pragma unroll
+        for (int s = 1; s < PER; s <<= 1) {
+#pragma unroll
+          for (int i = 0; i < PER; i++) {
+            if (!(i & s)) {
+              const float a = v[i], b = v[i + s];
+              v[i] = a + b;
+              v[i + s] = a - b;
+            }
           }
         }
+        // across lanes: channel c pairs with c ^ (ls * PER), stages in increasing bit order
+        auto stage = [&](auto ls_const) {
+          constexpr int LS = decltype(ls_const)::value;
+#pragma unroll
+          for (int i = 0; i < PER; i++) {
+            const float o = xshfl<LS>(v[i]);
+            v[i] = (l32 & LS) ? o - v[i] : v[i] + o;
+          }
+        };
+        stage(std::integral_constant<int, 1>{});
+        stage(std::integral_constant<int, 2>{});
+        stage(std::integral_constant<int, 4>{});
+        stage(std::integral_constant<int, 8>{});
+        stage(std::integral_constant<int, 16>{});
+        constexpr float rn = (float)inv_sqrt_hdim<HDIM>();
+#pragma unroll
+        for (int i = 0; i < PER; i++) v[i] *= rn;
       }
+      if constexpr (QK_T == T_I8) {
+        float amax = 0.0f;
 #pragma unroll
-      for (int ls = 1; ls < 32; ls <<= 1) {
+        for (int i = 0; i < PER; i++) amax = fmaxf(amax, fabsf(v[i]));
+        amax = fmaxf(amax, xshfl<16>(amax));
+        amax = fmaxf(amax, xshfl<8>(amax));
+        amax = fmaxf(amax, xshfl<4>(amax));
+        amax = fmaxf(amax, xshfl<2>(amax));
+        amax = fmaxf(amax, xshfl<1>(amax));
+        const float scale = amax > 0.0f ? amax / 127.0f : 1.0f;
+        typedef typename VecOf<PER, signed char>::type CV;
+        CV codes;
 #pragma unroll
-        for (int i = 0; i < PER; i++) {
-          const float o = __shfl_xor(v[i], ls);
-          v[i] = (l32 & ls) ? o - v[i] : v[i] + o;
-        }
+        for (int i = 0; i < PER; i++) codes[i] = (signed char)(int)rintf(v[i] / scale);
+        *(CV *)((isq ? Qo : Ko) + hrow * HDIM + l32 * PER) = codes;
+        if (l32 == rr) keep = scale;
+      } else {
+        using OE = typename Elem<QK_T>::type;
+        typedef typename VecOf<PER, OE>::type OV;
+        OV out;
+#pragma unroll
+        for (int i = 0; i < PER; i++) out[i] = (OE)v[i];
+        *(OV *)((isq ? Qo : Ko) + (hrow * HDIM + l32 * PER) * sizeof(OE)) = out;
       }
-      constexpr float rn = (float)inv_sqrt_hdim<HDIM>();
-#pragma unroll
-      for (int i = 0; i < PER; i++) v[i] *= rn;
-    }
-    const size_t hrow = isq ? ((size_t)sq * p.Hq + h) * p.out_rows + r : ((size_t)sq * p.Hk + h) * p.out_rows + r;
-    if constexpr (QK_T == T_I8) {
-      float amax = 0.0f;
-#pragma unroll
-      for (int i = 0; i < PER; i++) amax = fmaxf(amax, fabsf(v[i]));
-#pragma unroll
-      for (int s = 16; s >= 1; s >>= 1) amax = fmaxf(amax, __shfl_xor(amax, s));
-      const float scale = amax > 0.0f ? amax / 127.0f : 1.0f;
-      typedef typename VecOf<PER, signed char>::type CV;
-      CV codes;
-#pragma unroll
-      for (int i = 0; i < PER; i++) codes[i] = (signed char)(int)rintf(v[i] / scale);
-      *(CV *)((isq ? Qo : Ko) + hrow * HDIM + l32 * PER) = codes;
-      if (l32 == 0) (isq ? qsc : ksc)[hrow] = scale;
     } else {
-      using OE = typename Elem<QK_T>::type;
+      using OE = typename Elem<V_T>::type;
       typedef typename VecOf<PER, OE>::type OV;
       OV out;
 #pragma unroll
       for (int i = 0; i < PER; i++) out[i] = (OE)v[i];
-      *(OV *)((isq ? Qo : Ko) + (hrow * HDIM + l32 * PER) * sizeof(OE)) = out;
+      *(OV *)(Vo + (hrow * HDIM + l32 * PER) * sizeof(OE)) = out;
     }
-  } else {
-    using OE = typename Elem<V_T>::type;
-    typedef typename VecOf<PER, OE>::type OV;
-    OV out;
-#pragma unroll
-    for (int i = 0; i < PER; i++) out[i] = (OE)v[i];
-    const size_t vrow = ((size_t)sq * p.Hv + slot - p.Hq - p.Hk) * p.out_rows + r;
-    *(OV *)(Vo + (vrow * HDIM + l32 * PER) * sizeof(OE)) = out;
+  }
+  if constexpr (QK_T == T_I8) {
+    if (isqk && l32 < nr) (isq ? qsc : ksc)[hrow_of(m0 + l32)] = keep;
   }
 }
 
@@ -243,7 +287,7 @@ int launch_qk(const Pipeline &pl, hipStream_t stream, const Arg *a, int nargs, c
     return -1;
   if (QK_T == T_I8 && (!need(9, hq * 4, "q_scale", p.Hq > 0) || !need(10, hk * 4, "k_scale", p.Hk > 0))) return -1;
   if (p.M == 0) return 0;
-  dim3 grid((unsigned)p.M, (unsigned)((nslots + SLOTS_PER_WG - 1) / SLOTS_PER_WG));
+  dim3 grid((unsigned)((p.M + RPW - 1) / RPW), (unsigned)((nslots + SLOTS_PER_WG - 1) / SLOTS_PER_WG));
   hipLaunchKernelGGL((qk_norm_rope_kernel<HDIM, IN_T, QK_T, V_T, QKROT>), grid, dim3(256), 0, stream, a[0].ptr,
                      (const float *)a[1].ptr, (const float *)a[2].ptr, (const float *)a[3].ptr,
                      (const float *)a[4].ptr, a[5].ptr, a[6].ptr, a[7].ptr, nargs > 9 ? (float *)a[9].ptr : nullptr,
