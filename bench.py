@@ -1,7 +1,7 @@
 """Attention throughput on one MI355X: the BASELINE metric (attention TFLOP/s and % of the int8 MFMA peak at
 H=32, D=128, S=16896; ms per call).
 
-    python bench.py [--gpus 1] [--steps 20] [--warmup 3] [--config c4] [--no-cpu]
+    python bench.py [--gpus 1] [--steps 20] [--warmup 10] [--config c4] [--no-cpu]
 
 A step is one attention call over the whole workload (all heads, all query rows) with its inputs resident in
 HBM. The default workload is BASELINE config 4: B=1, H=32, D=128, S=16896 (512 text + 16384 image rows), Q/K bf16
@@ -122,7 +122,7 @@ def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=int(os.environ.get("WORLD_SIZE", "1")))
     ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--config", default="c4", choices=sorted(CONFIGS))
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--cpu-budget", type=float, default=20.0)

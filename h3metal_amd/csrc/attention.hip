@@ -470,9 +470,13 @@ __global__ __launch_bounds__(NW * 64) void attention_kernel(const char *__restri
   __syncthreads();
   if (grp == 1) __syncthreads();
   for (int j = 0; j <= nblk; j++) {
+    // The matrix phase runs at raised wave priority: when both waves of a SIMD are ready to issue, the MFMA
+    // stream (the longer dependency chain) goes first and the softmax VALU work fills the gaps.
+    __builtin_amdgcn_s_setprio(3);
     matrix_phase(j);
     if (j + 1 < nblk) store_k(j + 1);
     if (j < nblk) store_v(j);
+    __builtin_amdgcn_s_setprio(0);
     __syncthreads();
     load_k(j + 2);  // unconditional: blocks past L read as zeros, and the outstanding-load count stays exact
     load_v(j + 1);
