@@ -6,7 +6,8 @@ H=32, D=128, S=16896; ms per call).
 A step is one attention call over the whole workload (all heads, all query rows) with its inputs resident in
 HBM. The default workload is BASELINE config 4: B=1, H=32, D=128, S=16896 (512 text + 16384 image rows), Q/K bf16
 ~N(0,1) with 4 of 128 channels per head x20, rotated and quantised to int8 by the fused pre-pass (timed
-separately, reported under "prepass"), V bf16 ~N(0,1), int8 QK^T + bf16 P V. FLOPs follow the reference's
+separately, reported under "prepass"), V bf16 ~N(0,1), int8 QK^T + bf16 P V. The attention output's consumer,
+rot_q8 (256-block Hadamard + per-row int8 of O), is timed on the call's own output and reported under "rot_q8". FLOPs follow the reference's
 convention 4*H*Sq*Sk_valid*D (bench/attn_bench.py:27). The timed region is bracketed by stream
 synchronisations; GPU time comes from HIP events on the library's stream (h3_wait), per-launch durations from
 per-dispatch event pairs (profile mode). One JSON line is printed.
@@ -112,7 +113,8 @@ def traffic(kernel, cfg="c4"):
     if not os.path.exists(path) or CONFIGS_ARG.get("config") != cfg:
         return None
     with open(path) as f:
-        return int(json.load(f)[kernel]["traffic_bytes"])
+        d = json.load(f)
+    return int(d[kernel]["traffic_bytes"]) if kernel in d else None
 
 
 CONFIGS_ARG = {}
@@ -206,6 +208,18 @@ def main():
         nbytes = S * 3 * H * D * 2 + 2 * S * H * D + S * H * D * 2 + 2 * S * H * 4
         out["prepass"] = {"ms": round(pt * 1e3, 4), "bytes": nbytes, "GB/s": round(nbytes / pt / 1e9, 1),
                           "frac_hbm": round(nbytes / pt / HBM_PEAK, 4), "traffic": traffic("qk_norm_rope_kernel")}
+    # the attention output's consumer (h3metal/dit.py:209): rot_q8 of O [S][H*D] bf16 -> int8 + row scales
+    a8, sa = gpu.empty((S, H * D), "i8"), gpu.empty((S,), "f32")
+    ops.rot_q8(gpu, O, a8, sa, S, H * D)
+    gpu.profile(True)
+    for _ in range(args.steps):
+        ops.rot_q8(gpu, O, a8, sa, S, H * D)
+    gpu.wait()
+    rt = float(np.mean([t for _, t in gpu.profile_take()]))
+    gpu.profile(False)
+    rbytes = S * H * D * 2 + S * H * D + S * 4
+    out["rot_q8"] = {"ms": round(rt * 1e3, 4), "bytes": rbytes, "GB/s": round(rbytes / rt / 1e9, 1),
+                     "frac_hbm": round(rbytes / rt / HBM_PEAK, 4), "traffic": traffic("rot_q8_kernel")}
     if not args.no_cpu:
         out["cpu_baseline"] = cpu_baseline(args.config, L, args.cpu_budget)
     gpu.close()

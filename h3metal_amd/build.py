@@ -6,8 +6,9 @@ Each source compiles to an object in h3metal_amd/_build/ in parallel, then one
 shared library is linked next to this file, where gpu.py loads it. Flags:
   * --offload-arch=gfx950 only (CDNA4; no other targets),
   * packed fp32 instructions disabled (-target-feature -packed-fp32-ops),
-  * the pre-pass without FMA contraction, so its float32 steps are the
-    separately rounded operations a CPU restatement reproduces bit for bit.
+  * the row kernels (pre-pass, rot_q8) without FMA contraction, so their
+    float32 steps are the separately rounded operations a CPU restatement
+    reproduces bit for bit.
 """
 
 from __future__ import annotations
@@ -27,8 +28,9 @@ COMMON = ["--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC", "-Wall", "-Wno-
           "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
 PER_FILE = {
     "qk_prepass.hip": ["-ffp-contract=off"],
+    "rot_q8.hip": ["-ffp-contract=off"],
 }
-SOURCES = ["capi.hip", "attention.hip", "qk_prepass.hip"]
+SOURCES = ["capi.hip", "attention.hip", "qk_prepass.hip", "rot_q8.hip"]
 
 
 def hipcc() -> str:

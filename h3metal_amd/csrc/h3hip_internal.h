@@ -4,6 +4,7 @@
 // pack them with struct exactly as the reference does:
 //   AttnParams   <- kernels/params.h:41-53, packed by h3metal/ops.py:187-188 ("7if3i")
 //   QkRopeParams <- kernels/ops.metal:344-349, packed by h3metal/ops.py:237 ("8ifi")
+//   RotQParams   <- kernels/params.h:25-29, packed by h3metal/ops.py:221 ("4i")
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -36,6 +37,13 @@ struct QkRopeParams {
 };
 static_assert(sizeof(QkRopeParams) == 40, "QkRopeParams must match struct.pack('<8ifi')");
 
+struct RotQParams {
+  int M, D;      // rows, features (a multiple of 256)
+  int x_stride;  // elements between rows of the input
+  int mode;      // 0: input as is; 1: input rows hold [value | gate], the row is value * silu(gate)
+};
+static_assert(sizeof(RotQParams) == 16, "RotQParams must match struct.pack('<4i')");
+
 using Macros = std::map<std::string, std::string>;
 
 // One bound buffer argument as the launchers see it: a device address and the
@@ -60,6 +68,17 @@ struct Pipeline {
 // Module factories: fill `pl` for (fn, macros) or return false with a message.
 bool make_attention(const std::string &fn, const Macros &m, Pipeline *pl, std::string *err);
 bool make_ops(const std::string &fn, const Macros &m, Pipeline *pl, std::string *err);
+bool make_rot_q8(const Macros &m, Pipeline *pl, std::string *err);  // module "ops", function "rot_q8"
+
+// Wave64 lane exchanges inside a 32-lane half wave, shared by the row kernels: the value of lane (lane ^ S).
+// DPP for S = 1, 2 (quad_perm), ds_swizzle's xor mode (no LDS memory access) for S = 4, 8, 16.
+template <int S>
+__device__ __forceinline__ float xshfl(float v) {
+  const int x = __builtin_bit_cast(int, v);
+  if constexpr (S == 1) return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, x, 0xB1, 0xF, 0xF, false));
+  else if constexpr (S == 2) return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, x, 0x4E, 0xF, 0xF, false));
+  else return __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(x, 0x1F | (S << 10)));
+}
 
 // Helpers for macro parsing in the factories.
 bool macro_int(const Macros &m, const char *key, int def, int *out, std::string *err);

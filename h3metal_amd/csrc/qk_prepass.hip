@@ -55,15 +55,6 @@ constexpr double inv_sqrt_hdim() {
   return HDIM == 128 ? 0.0883883476483184405501055452631 : HDIM == 64 ? 0.125 : 0.1767766952966368811;
 }
 
-// v from lane (lane ^ S) of the same 32-lane half: DPP for S = 1, 2, ds_swizzle (no memory access) for 4, 8, 16.
-template <int S>
-__device__ __forceinline__ float xshfl(float v) {
-  const int x = __builtin_bit_cast(int, v);
-  if constexpr (S == 1) return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, x, 0xB1, 0xF, 0xF, false));
-  else if constexpr (S == 2) return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, x, 0x4E, 0xF, 0xF, false));
-  else return __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(x, 0x1F | (S << 10)));
-}
-
 // Workgroup (bx, by): rows bx*RPW .. bx*RPW + RPW-1, slots by*8 .. by*8 + 7. A half wave owns one slot and
 // walks the rows; lane l32 keeps the scale of row l32 so that a slot's RPW scales (consecutive in memory within
 // a sequence) are stored together after the rows.
@@ -333,8 +324,9 @@ int type_of(const std::string &s) {
 // half | bfloat, default half as in the reference), V_T (half | bfloat, default
 // half). NSG (the reference's SIMD-groups per threadgroup) is accepted and unused.
 bool make_ops(const std::string &fn, const Macros &m, Pipeline *pl, std::string *err) {
+  if (fn == "rot_q8") return make_rot_q8(m, pl, err);
   if (fn != "qk_norm_rope") {
-    *err = "unknown function (have: qk_norm_rope)";
+    *err = "unknown function (have: qk_norm_rope, rot_q8)";
     return false;
   }
   int hd, q8, rot, nsg;

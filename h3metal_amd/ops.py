@@ -1,11 +1,12 @@
 """Launchers of the attention path: one Python function per GPU operation.
 
-Drop-in for the two launchers of the reference's h3metal/ops.py on the DiT
+Drop-in for the launchers of the reference's h3metal/ops.py on the DiT
 attention path, with the same arguments, buffer layouts, parameter blocks and
 return value (None; results are valid after `gpu.wait()`):
 
   attention     <- h3metal/ops.py:177-191
   qk_norm_rope  <- h3metal/ops.py:225-239
+  rot_q8        <- h3metal/ops.py:214-222 (the consumer of the attention output, h3metal/dit.py:209)
   pad_rows      <- h3metal/ops.py:116-117
 
 Element types come from the tensors, as in the reference (`OUT_DT`,
@@ -84,3 +85,25 @@ def qk_norm_rope(gpu: Gpu, qkv: Tensor, wq: Tensor | None, wk: Tensor | None, co
     slots = Hq + Hk + Hv
     params = pack("8ifi", M, Hq, Hk, Hv, in_stride or slots * hd, out_rows, rot, int(norm), eps, seq_len or M)
     gpu.launch(k, None, None, [qkv, wq, wk, cos, sin, Q, K, V, None, q_scale, k_scale], params, params_index=8)
+
+
+def _rows_kernel_cfg(D: int):
+    """SIMD-groups and rotation blocks per SIMD-group of the reference's row kernels (h3metal/ops.py:193-197);
+    passed as the NSG / MAXB specialisation, which bounds the row length (NSG * MAXB * 256 columns)."""
+    nb = D // 256
+    nsg = 8 if nb >= 8 else nb
+    return nsg, -(-nb // nsg)
+
+
+def rot_q8(gpu: Gpu, x: Tensor, out: Tensor, sa: Tensor | None, M: int, D: int, *, swiglu: bool = False,
+           x_stride: int | None = None, out_hr: bool = False):
+    """out = int8(rot(x)) (or of value * silu(gate) with the gates in columns D..2D-1) and its row scales;
+    with out_hr the rotated rows in half precision instead. rot multiplies every 256-column block by the
+    orthonormal 256-point Walsh-Hadamard matrix. x [M][x_stride] (f16 / bf16 / f32), out [M][D] i8 (f16 with
+    out_hr), sa [M] f32."""
+    if D < 256 or D % 256:
+        raise ValueError(f"rot_q8: D must be a positive multiple of 256, got {D}")
+    nsg, maxb = _rows_kernel_cfg(D)
+    k = gpu.kernel("ops", "rot_q8", NSG=nsg, MAXB=maxb, IN_T=OUT_DT[x.dtype], OUT_HR=int(out_hr))
+    params = pack("4i", M, D, x_stride or (2 * D if swiglu else D), 1 if swiglu else 0)
+    gpu.launch(k, None, None, [x, out, sa], params)

@@ -7,6 +7,9 @@ missing.
 
   oracle.prepass    float32 op-by-op restatement of qk_norm_rope
                     (reference kernels/ops.metal:365-468)
+  oracle.rot_q8     float32 op-by-op restatement of rot_q8, the row rotation +
+                    int8 that consumes the attention output
+                    (reference kernels/ops.metal:272-334)
   oracle.attention  float64 softmax attention (reference tests/test_attention.py:9-21)
                     and exact integer scores
   oracle.bf16       bf16 <-> float32 conversions (round to nearest even)

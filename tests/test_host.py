@@ -106,6 +106,23 @@ def test_qk_norm_rope_launcher_packs_reference_params():
     assert g2.kernels[0][2]["QKROT"] == 0 and g2.kernels[0][2]["QK_T"] == "half"
 
 
+def test_rot_q8_launcher_packs_reference_params():
+    """h3metal/ops.py:214-222: NSG/MAXB from the row length, IN_T from the input, pack("4i", M, D, x_stride,
+    mode) with x_stride defaulting to 2D under swiglu; buffers [x, out, sa]."""
+    g = FakeGpu()
+    x, out, sa = T((19, 2 * 14336), "bf16"), T((19, 14336), "i8"), T((19,), "f32")
+    ops.rot_q8(g, x, out, sa, 19, 14336, swiglu=True)
+    ops.rot_q8(g, T((7, 4096), "f16"), T((7, 4096), "f16"), None, 7, 1024, x_stride=4096, out_hr=True)
+    (f1, n1, m1), (f2, n2, m2) = g.kernels
+    assert (f1, n1) == ("ops", "rot_q8") and m1 == {"NSG": 8, "MAXB": 7, "IN_T": "bfloat", "OUT_HR": 0}
+    assert m2 == {"NSG": 4, "MAXB": 1, "IN_T": "half", "OUT_HR": 1}
+    (_, a1, p1, i1), (_, a2, p2, i2) = g.launches
+    assert a1 == [x, out, sa] and struct.unpack("<4i", p1) == (19, 14336, 2 * 14336, 1)
+    assert a2[2] is None and struct.unpack("<4i", p2) == (7, 1024, 4096, 0)
+    with pytest.raises(ValueError):
+        ops.rot_q8(g, x, out, sa, 19, 1000)
+
+
 def test_pack_and_pad_rows():
     assert len(G.pack("7if3i", *range(7), 1.0, 0, 1, 2)) == 44  # sizeof(AttnParams), csrc/h3hip_internal.h
     assert len(G.pack("8ifi", *range(8), 1e-6, 5)) == 40         # sizeof(QkRopeParams)

@@ -242,3 +242,69 @@ def test_golden_prepass_fixture_reproduces():
 def test_golden_scores_fixture_reproduces():
     f = np.load(os.path.join(GOLDEN, "scores_int8.npz"))
     assert np.array_equal(oa.int_scores(f["Q"], f["K"]), f["S"])
+
+
+# -- rot_q8 (the attention output's consumer) ------------------------------------------------------------------------
+
+def test_rot_rows_matches_reference_test_formula():
+    """The reference's own check (tests/test_ops.py:9-18): x.reshape(M, D/256, 256) @ H^T / sqrt(256) with the
+    Sylvester matrix, in float64."""
+    from oracle import rot_q8 as orq
+    rng = np.random.default_rng(5)
+    x = (rng.standard_normal((9, 1024)) * 2).astype(np.float32)
+    want = (x.astype(np.float64).reshape(9, 4, 256) @ sylvester(256).T / 16.0).reshape(9, 1024)
+    got = orq.rotate_rows_f32(x).astype(np.float64)
+    np.testing.assert_allclose(got, want, rtol=0, atol=2e-6 * np.abs(want).max())
+
+
+def test_rot_rows_blocks_independent_and_one_hot():
+    """A one-hot column c of block b yields +-1/16 exactly in block b only, with the signs of Sylvester row
+    c % 256 (a block mix-up or a wrong stage order fails)."""
+    from oracle import rot_q8 as orq
+    D = 768
+    for c in (0, 1, 37, 255, 256 + 130, 512 + 7):
+        x = np.zeros((1, D), np.float32)
+        x[0, c] = 1.0
+        r = orq.rotate_rows_f32(x)[0]
+        b = c // 256
+        assert np.all(r[:b * 256] == 0) and np.all(r[(b + 1) * 256:] == 0)
+        assert np.array_equal(r[b * 256:(b + 1) * 256], (sylvester(256)[c % 256] / 16).astype(np.float32))
+
+
+def test_rot_rows_integer_exact_and_involution():
+    """Integer rows: every butterfly sum is exact, so the result is the integer matrix product / 16 bit for bit;
+    the rotation is orthonormal and symmetric, so applying it twice returns the row."""
+    from oracle import rot_q8 as orq
+    rng = np.random.default_rng(6)
+    x = rng.integers(-500, 500, (5, 512))
+    want = (x.reshape(5, 2, 256) @ sylvester(256).astype(np.int64).T).reshape(5, 512) / 16.0
+    assert np.array_equal(orq.rotate_rows_f32(x.astype(np.float32)), want.astype(np.float32))
+    y = rng.standard_normal((5, 512)).astype(np.float32)
+    np.testing.assert_allclose(orq.rotate_rows_f32(orq.rotate_rows_f32(y)), y, rtol=0, atol=1e-5)
+
+
+def test_rot_q8_int8_step():
+    """Row scale = amax/127 of the rotated row: the largest entry codes to +-127, every code dequantises within
+    half a step, a zero row gets scale 1 and zero codes; swiglu with zero gates is the zero row."""
+    from oracle import rot_q8 as orq
+    rng = np.random.default_rng(7)
+    x = (rng.standard_normal((6, 512)) * 3).astype(np.float32)
+    x[2] = 0
+    codes, scale, r = orq.rot_q8(x, 512)
+    assert scale[2] == 1 and not codes[2].any()
+    for m in (0, 1, 3, 4, 5):
+        j = np.abs(r[m]).argmax()
+        assert abs(int(codes[m, j])) == 127
+        assert np.abs(codes[m].astype(np.float64) * scale[m] - r[m]).max() <= 0.5 * scale[m] * (1 + 1e-6)
+    xs = np.concatenate([x, np.zeros_like(x)], 1)
+    c2, s2, _ = orq.rot_q8(xs, 512, swiglu=True)
+    assert np.all(s2 == 1) and not c2.any()
+
+
+def test_silu_gate_against_float64():
+    from oracle import rot_q8 as orq
+    rng = np.random.default_rng(8)
+    x = (rng.standard_normal((4, 512)) * 4).astype(np.float32)
+    v, g = x[:, :256].astype(np.float64), x[:, 256:].astype(np.float64)
+    want = v * g / (1 + np.exp(-g))
+    np.testing.assert_allclose(orq.silu_gated_f32(x, 256), want, rtol=3e-6, atol=1e-6)
