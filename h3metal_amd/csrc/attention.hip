@@ -173,12 +173,16 @@ constexpr float MAGICF = 12582912.0f;
 
 // DUMP: instead of attention, write the raw score accumulators S[h][q][key]
 // (int32 for int8 inputs, fp32 otherwise) of the same MFMA path, for tests.
-template <int D, int QKT, int VT, int OT, bool CAUSAL, bool DUMP>
+template <int DG, int QKT, int VT, int OT, bool CAUSAL, bool DUMP>
 __global__ __launch_bounds__(NW * 64) void attention_kernel(const char *__restrict__ Q, const char *__restrict__ K,
                                                             const char *__restrict__ V, char *__restrict__ O,
                                                             const float *__restrict__ qs,
                                                             const float *__restrict__ ks, AttnParams p, int nqb) {
+  // DG: the head dim of the tensors in memory; D: the head dim computed with (96 runs as 128: the missing
+  // channels load as zeros, which changes no score and no output channel that is stored).
+  constexpr int D = DG == 96 ? 128 : DG;
   using C = Cfg<D, QKT>;
+  constexpr int RBG = DG * C::ESZ;  // bytes per Q/K row in memory
   using VT8 = typename Vec8<VT>::type;
   using VE = typename Vec8<VT>::elem;
   using VP2 = typename Vec8<VT>::pair;
@@ -200,18 +204,20 @@ __global__ __launch_bounds__(NW * 64) void attention_kernel(const char *__restri
   // Q operand (B of S^T = K Q^T): row q, piece 2c + hl of each 32-byte chunk c.
   i32x4 qreg[C::NCH];
   {
-    const char *qrow = Q + ((size_t)h * p.q_rows + (qvalid ? q : 0)) * C::RB;
+    const char *qrow = Q + ((size_t)h * p.q_rows + (qvalid ? q : 0)) * RBG;
 #pragma unroll
     for (int c = 0; c < C::NCH; c++) {
-      const i32x4 v = *(const i32x4 *)(qrow + (2 * c + hl) * 16);
-      qreg[c] = qvalid ? v : i32x4{0, 0, 0, 0};
+      const int pc = 2 * c + hl;
+      const bool in_row = pc * 16 < RBG;  // always true unless DG < D
+      const i32x4 v = *(const i32x4 *)(qrow + (in_row ? pc : 0) * 16);
+      qreg[c] = qvalid && in_row ? v : i32x4{0, 0, 0, 0};
     }
   }
   float qsc = p.scale;
   if constexpr (C::QK8) qsc = qvalid ? fmaxf(qs[(size_t)h * p.q_rows + q] * p.scale, FLT_MIN) : 1.0f;
 
-  const char *Kh = K + (size_t)kvh * p.k_rows * C::RB;
-  const char *Vh = V + (size_t)kvh * p.k_rows * D * 2;
+  const char *Kh = K + (size_t)kvh * p.k_rows * RBG;
+  const char *Vh = V + (size_t)kvh * p.k_rows * DG * 2;
   const float *ksh = C::QK8 ? ks + (size_t)kvh * p.k_rows : nullptr;
   int kend = p.L;
   if constexpr (CAUSAL) kend = min(p.L, qb * C::BQ + C::BQ + p.causal_off);
@@ -235,21 +241,26 @@ __global__ __launch_bounds__(NW * 64) void attention_kernel(const char *__restri
                                              rows * row_bytes, 0x00020000);
   };
   auto load_k = [&](int blk) {
-    const __amdgpu_buffer_rsrc_t r = rsrc(Kh, blk, C::RB);
+    const __amdgpu_buffer_rsrc_t r = rsrc(Kh, blk, RBG);
 #pragma unroll
     for (int i = 0; i < KPT; i++) {
       const int idx = (gt + i * GT) % (HK * C::NP);
-      kr[i] = __builtin_amdgcn_raw_buffer_load_b128(r, (row0 + idx / C::NP) * C::RB + (idx % C::NP) * 16, 0, 0);
+      // pieces past a row in memory (DG < D) are sent out of the descriptor's range: they read as zero
+      const int pc = idx % C::NP;
+      const unsigned off = pc * 16 < RBG ? (row0 + idx / C::NP) * RBG + pc * 16 : 0x80000000u;
+      kr[i] = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
     }
     if constexpr (C::QK8)
       ksr = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rsrc(ksh, blk, 4), (row0 + (gt & (HK - 1))) * 4, 0, 0));
   };
   auto load_v = [&](int blk) {
-    const __amdgpu_buffer_rsrc_t r = rsrc(Vh, blk, D * 2);
+    const __amdgpu_buffer_rsrc_t r = rsrc(Vh, blk, DG * 2);
 #pragma unroll
     for (int i = 0; i < VPT; i++) {
       const int idx = (gt + i * GT) % (HK * C::VP);
-      vr[i] = __builtin_amdgcn_raw_buffer_load_b128(r, (row0 + idx / C::VP) * D * 2 + (idx % C::VP) * 16, 0, 0);
+      const int pc = idx % C::VP;
+      const unsigned off = pc * 16 < DG * 2 ? (row0 + idx / C::VP) * DG * 2 + pc * 16 : 0x80000000u;
+      vr[i] = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
     }
   };
   auto store_k = [&](int blk) {
@@ -490,9 +501,9 @@ __global__ __launch_bounds__(NW * 64) void attention_kernel(const char *__restri
     if (qvalid) {
       constexpr int OSZ = OT == T_F32 ? 4 : 2;
       const int seq = h / p.seq_heads;
-      char *orow = O + (((size_t)seq * p.seq_rows + q) * p.o_stride + (size_t)(h - seq * p.seq_heads) * D) * OSZ;
+      char *orow = O + (((size_t)seq * p.seq_rows + q) * p.o_stride + (size_t)(h - seq * p.seq_heads) * DG) * OSZ;
 #pragma unroll
-      for (int db = 0; db < D / 32; db++)
+      for (int db = 0; db < DG / 32; db++)
 #pragma unroll
         for (int g = 0; g < 4; g++) {
           const int d = db * 32 + 8 * g + 4 * hl;
@@ -510,7 +521,7 @@ int esize(int t) { return t == T_I8 ? 1 : t == T_F32 ? 4 : 2; }
 template <int D, int QKT, int VT, int OT, bool CAUSAL, bool DUMP>
 int launch_attention(const Pipeline &pl, hipStream_t stream, const Arg *args, int nargs, const void *params,
                      uint32_t params_len, std::string *err) {
-  using C = Cfg<D, QKT>;
+  using C = Cfg<D == 96 ? 128 : D, QKT>;  // D: the head dim in memory
   if (params_len != sizeof(AttnParams)) {
     *err = "parameter block of " + std::to_string(params_len) + " bytes, expected " +
            std::to_string(sizeof(AttnParams));
@@ -629,7 +640,8 @@ int type_of(const std::string &s) {
 
 }  // namespace
 
-// Specialisation macros: HD (head dim: 64 or 128), QK8 (int8 scores), O_T
+// Specialisation macros: HD (head dim: 64, 96 or 128; 96 is the vision tower's
+// padded head dim, h3metal/vision.py:34, 129), QK8 (int8 scores), O_T
 // (output: half | bfloat | float), CAUSAL, and IN_T (half | bfloat: the type of
 // V, and of Q and K without QK8; the reference's inputs are half). The
 // reference's tuning macros WM, BK, KPAD, DB, PVORDER, VX, SLACK are accepted
@@ -662,13 +674,14 @@ bool make_attention(const std::string &fn, const Macros &m, Pipeline *pl, std::s
     *err = "O_T must be half|bfloat|float and IN_T half|bfloat";
     return false;
   }
-  if (hd != 64 && hd != 128) {
-    *err = "HD " + std::to_string(hd) + " not supported (64 or 128)";
+  if (hd != 64 && hd != 96 && hd != 128) {
+    *err = "HD " + std::to_string(hd) + " not supported (64, 96 or 128)";
     return false;
   }
   const int qkt = qk8 ? T_I8 : it;
   LaunchFn f;
   if (hd == 128) f = dump ? pick_types<128, true>(qkt, it, ot, causal) : pick_types<128, false>(qkt, it, ot, causal);
+  else if (hd == 96) f = dump ? pick_types<96, true>(qkt, it, ot, causal) : pick_types<96, false>(qkt, it, ot, causal);
   else f = dump ? pick_types<64, true>(qkt, it, ot, causal) : pick_types<64, false>(qkt, it, ot, causal);
   pl->launch = f;
   pl->threads = NW * 64;

@@ -316,3 +316,85 @@ def test_config4_int8_rotated_full_size(gpu):
     got = from_bf16(O.numpy()).astype(np.float64)[rows]
     err = np.abs(got - ref)
     assert err.max() < NS_MAX and err.mean() < NS_MEAN, (err.max(), err.mean())
+
+
+# -- other callers' variants -----------------------------------------------------------------------------
+
+@pytest.mark.parametrize("dtype,H,KVH,causal", [("f16", 4, 2, False), ("f16", 4, 4, True), ("bf16", 3, 3, False)])
+def test_head_dim_96(gpu, dtype, H, KVH, causal):
+    """Head dim 96, the vision tower's padded head dim (h3metal/vision.py:34, 121-130): computed on 128-wide
+    MFMA tiles with the missing channels read as zeros."""
+    rng = np.random.default_rng(31)
+    Lq, L, D = 150, 220, 96
+    q = rng.standard_normal((H, Lq, D)).astype(np.float32)
+    k, v = (rng.standard_normal((KVH, L, D)).astype(np.float32) for _ in range(2))
+    if dtype == "bf16":
+        qh, kh, vh = to_bf16(q), to_bf16(k), to_bf16(v)
+        qf, kf, vf = from_bf16(qh), from_bf16(kh), from_bf16(vh)
+    else:
+        qh, kh, vh = q.astype(np.float16), k.astype(np.float16), v.astype(np.float16)
+        qf, kf, vf = qh, kh, vh
+    got = run_attention(gpu, qh, kh, vh, dtype=dtype, Lq=Lq, L=L, H=H, KVH=KVH, D=D, scale=D ** -0.5,
+                        causal=causal)
+    ref = oa.ref_attention(qf, kf, vf, D ** -0.5, causal=causal)
+    err = np.abs(got[:Lq] - ref)
+    assert err.max() < (5e-3 if dtype == "f16" else NS_MAX) and err.mean() < NS_MEAN, (err.max(), err.mean())
+
+
+def test_head_dim_96_vision_padding(gpu):
+    """vision.py pads head dim 72 to 96 with zero channels: the output's padded channels stay exactly zero and the
+    real ones equal attention over the 72 real channels with scale 72^-0.5."""
+    rng = np.random.default_rng(32)
+    H, N, hd, hdp = 2, 100, 72, 96
+    q, k, v = (np.zeros((H, N, hdp), np.float16) for _ in range(3))
+    for t in (q, k, v):
+        t[..., :hd] = rng.standard_normal((H, N, hd)).astype(np.float16)
+    got = run_attention(gpu, q, k, v, dtype="f16", Lq=N, L=N, H=H, KVH=H, D=hdp, scale=hd ** -0.5)
+    got = got[:N].reshape(N, H, hdp)
+    assert (got[..., hd:] == 0).all()
+    ref = oa.ref_attention(q[..., :hd], k[..., :hd], v[..., :hd], hd ** -0.5).reshape(N, H, hd)
+    assert np.abs(got[..., :hd] - ref).max() < 5e-3
+
+
+def test_int8_head_dim_96_scores_and_output(gpu):
+    rng = np.random.default_rng(33)
+    H, Lq, L, D = 2, 130, 190, 96
+    qi, qs = q8(rng.standard_normal((H, Lq, D)).astype(np.float32))
+    ki, ks = q8(rng.standard_normal((H, L, D)).astype(np.float32))
+    Q, K = padded(gpu, qi, 192, "i8"), padded(gpu, ki, 192, "i8")
+    S = gpu.empty((H, Lq, L), "i32")
+    ops.attention_scores(gpu, Q, K, gpu.empty((H, 192, D), "bf16"), S, Lq=Lq, L=L, H=H, KVH=H, D=D, q_rows=192,
+                         k_rows=192, q_scale=padded(gpu, qs, 192, "f32"), k_scale=padded(gpu, ks, 192, "f32"))
+    gpu.wait()
+    assert np.array_equal(S.numpy(), oa.int_scores(qi, ki))
+    v = to_bf16(rng.standard_normal((H, L, D)).astype(np.float32))
+    got = run_attention(gpu, qi, ki, v, dtype="bf16", Lq=Lq, L=L, H=H, KVH=H, D=D, scale=D ** -0.5, qs=qs, ks=ks)
+    ref = oa.ref_attention(qi * qs[..., None].astype(np.float64), ki * ks[..., None].astype(np.float64),
+                           from_bf16(v), D ** -0.5)
+    err = np.abs(got[:Lq] - ref)
+    assert err.max() < NS_MAX and err.mean() < NS_MEAN
+
+
+def test_te_n_valid_split_dispatch(gpu):
+    """h3metal/te.py:186-194: with n_valid < T, a causal call over the first n_valid rows and keys, then a
+    non-causal call for rows n_valid..T-1 through a Q view and an output row view, attending to the n_valid keys;
+    GQA with Hq = 8, Hkv = 2, half inputs and output."""
+    rng = np.random.default_rng(34)
+    Hq, Hkv, T, n_valid, hd = 8, 2, 200, 130, 128
+    Tp = 256
+    q = rng.standard_normal((Hq, T, hd)).astype(np.float16)
+    k, v = (rng.standard_normal((Hkv, T, hd)).astype(np.float16) for _ in range(2))
+    Q, K, V = padded(gpu, q, Tp, "f16"), padded(gpu, k, Tp, "f16"), padded(gpu, v, Tp, "f16")
+    o = gpu.empty((Tp, Hq * hd), "f16")
+    ops.attention(gpu, Q, K, V, o, Lq=n_valid, L=n_valid, H=Hq, KVH=Hkv, D=hd, q_rows=Tp, k_rows=Tp,
+                  scale=hd ** -0.5, causal=True, wm=8, bk=32)
+    ops.attention(gpu, Q.view(Q.shape, offset_elems=n_valid * hd), K, V, o.row(n_valid, T - n_valid),
+                  Lq=T - n_valid, L=n_valid, H=Hq, KVH=Hkv, D=hd, q_rows=Tp, k_rows=Tp, scale=hd ** -0.5,
+                  causal=False, wm=8, bk=32)
+    gpu.wait()
+    got = o.numpy().astype(np.float64)
+    ref_a = oa.ref_attention(q[:, :n_valid], k[:, :n_valid], v[:, :n_valid], hd ** -0.5, causal=True)
+    ref_b = oa.ref_attention(q[:, n_valid:], k[:, :n_valid], v[:, :n_valid], hd ** -0.5)
+    assert np.abs(got[:n_valid] - ref_a).max() < 5e-3
+    assert np.abs(got[n_valid:T] - ref_b).max() < 5e-3
+    assert (got[T:] == 0).all()
