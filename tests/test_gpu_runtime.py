@@ -33,8 +33,8 @@ def test_unknown_kernel_and_macros(gpu):
         gpu.kernel("gemm", "gemm")
     with pytest.raises(GpuError, match="unknown function"):
         gpu.kernel("attention", "nope")
-    with pytest.raises(GpuError, match="HD 96"):
-        gpu.kernel("attention", "attention", HD=96)
+    with pytest.raises(GpuError, match="HD 80"):
+        gpu.kernel("attention", "attention", HD=80)
     with pytest.raises(GpuError, match="unknown macro"):
         gpu.kernel("attention", "attention", FOO=1)
     with pytest.raises(GpuError, match="QKROT needs QK8"):
