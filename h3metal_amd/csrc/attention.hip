@@ -158,16 +158,15 @@ struct Cfg {
   static constexpr int KOFF = 0;                          // K ring: 2 blocks
   static constexpr int VOFF = 2 * KBYTES;                 // V ring: 2 blocks
   static constexpr int SOFF = VOFF + 2 * VBYTES;          // key-scale ring: 3 blocks
-  static constexpr int NOFF = SOFF + 3 * BK * 4;          // -C * key-scale ring: 3 blocks
-  static constexpr int LDS = QK8 ? NOFF + 3 * BK * 4 : SOFF;
+  static constexpr int LDS = QK8 ? SOFF + 3 * BK * 4 : SOFF;
   static_assert(D % 32 == 0 && D <= 128, "head dim");
 };
 
 // int8 scores: the int32 accumulators start at MAGIC, the bit pattern of the float 1.5 * 2^23. Adding a score
 // s (|s| <= 128 * 127^2 < 2^22) keeps the sum in the binade [2^23, 2^24), where the float with those bits is
-// exactly 1.5 * 2^23 + s. So s * ks = fma(float_bits(acc), ks, -1.5 * 2^23 * ks), one full-rate instruction
-// instead of a half-rate int->float conversion and a multiply (the rounding of -1.5 * 2^23 * ks moves the score
-// by at most 0.75 integer units; the int32 accumulator itself stays exact).
+// exactly 1.5 * 2^23 + s. So s = float_bits(acc) - 1.5 * 2^23 exactly, a full-rate subtraction instead of a
+// half-rate int->float conversion, and s * ks is one rounding. (Folding the subtraction into an fma with a
+// per-key -1.5 * 2^23 * ks saves the subtraction but costs a second LDS vector per key, which measured slower.)
 constexpr int MAGIC = 0x4B400000;
 constexpr float MAGICF = 12582912.0f;
 
@@ -274,7 +273,6 @@ __global__ __launch_bounds__(NW * 64) void attention_kernel(const char *__restri
     if constexpr (C::QK8) {
       if (gt < HK) {
         ((float *)(smem + C::SOFF))[(blk % 3) * BK + row0 + gt] = ksr;
-        ((float *)(smem + C::NOFF))[(blk % 3) * BK + row0 + gt] = -MAGICF * ksr;
       }
     }
   };
@@ -387,9 +385,8 @@ __global__ __launch_bounds__(NW * 64) void attention_kernel(const char *__restri
     // element i of lane-half hl holds key kb + 32 t + 16 (i / 8) + 8 hl + i % 8
     if constexpr (C::QK8) {
       const float *ksc = (const float *)(smem + C::SOFF) + (j % 3) * BK;
-      const float *nbc = (const float *)(smem + C::NOFF) + (j % 3) * BK;
       // all key scales of the block first: one LDS round trip instead of one per group of four keys
-      f32x4 k4[2][2][2], n4[2][2][2];
+      f32x4 k4[2][2][2];
 #pragma unroll
       for (int t = 0; t < 2; t++)
 #pragma unroll
@@ -398,7 +395,6 @@ __global__ __launch_bounds__(NW * 64) void attention_kernel(const char *__restri
           for (int hh = 0; hh < 2; hh++) {
             const int off = 32 * t + 16 * s8 + 8 * hl + 4 * hh;
             k4[t][s8][hh] = *(const f32x4 *)(ksc + off);
-            n4[t][s8][hh] = *(const f32x4 *)(nbc + off);
           }
 #pragma unroll
       for (int t = 0; t < 2; t++) {
@@ -411,7 +407,7 @@ __global__ __launch_bounds__(NW * 64) void attention_kernel(const char *__restri
 #pragma unroll
             for (int e = 0; e < 4; e++) {
               const int i = 8 * s8 + 4 * hh + e;
-              x[t][i] = fmaf(sf[i], k4[t][s8][hh][e], n4[t][s8][hh][e]);
+              x[t][i] = (sf[i] - MAGICF) * k4[t][s8][hh][e];
             }
       }
     } else {
