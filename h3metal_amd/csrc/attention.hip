@@ -48,9 +48,12 @@
 //    range of (head, query-block) tiles, which then share one head's K/V in L2.
 #include "h3hip_internal.h"
 
+#include <algorithm>
 #include <cfloat>
 #include <cmath>
 #include <cstring>
+#include <map>
+#include <mutex>
 #include <type_traits>
 
 namespace h3 {
@@ -170,13 +173,25 @@ struct Cfg {
 constexpr int MAGIC = 0x4B400000;
 constexpr float MAGICF = 12582912.0f;
 
+// Tail split: when the last round of workgroups would leave CUs idle, its tiles (the last tiles in tile order)
+// are cut along the keys into `s` chunks of `cb` key blocks each, one workgroup per chunk. A chunk writes its
+// unnormalised partial state (O, running maximum m, row sum l) to `ws`, row stride DG + 4 floats (O at 0,
+// m at DG, l at DG + 1), and attention_merge combines the chunks of a tile.
+struct Split {
+  int nfull;  // workgroups that run whole tiles (tiles 0 .. nfull-1)
+  int s;      // chunks per split tile (0: no split)
+  int cb;     // key blocks per chunk
+  float *ws;  // partial states: [unit][BQ rows][DG + 4]
+};
+
 // DUMP: instead of attention, write the raw score accumulators S[h][q][key]
 // (int32 for int8 inputs, fp32 otherwise) of the same MFMA path, for tests.
 template <int DG, int QKT, int VT, int OT, bool CAUSAL, bool DUMP>
 __global__ __launch_bounds__(NW * 64) void attention_kernel(const char *__restrict__ Q, const char *__restrict__ K,
                                                             const char *__restrict__ V, char *__restrict__ O,
                                                             const float *__restrict__ qs,
-                                                            const float *__restrict__ ks, AttnParams p, int nqb) {
+                                                            const float *__restrict__ ks, AttnParams p, int nqb,
+                                                            Split sp) {
   // DG: the head dim of the tensors in memory; D: the head dim computed with (96 runs as 128: the missing
   // channels load as zeros, which changes no score and no output channel that is stored).
   constexpr int D = DG == 96 ? 128 : DG;
@@ -191,10 +206,18 @@ __global__ __launch_bounds__(NW * 64) void attention_kernel(const char *__restri
   const int tid = threadIdx.x, lane = tid & 63, hl = lane >> 5, l32 = lane & 31;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: keeps the group branches scalar
   const int grp = w >> 2;  // 0: matrix phase first in each key block, 1: vector phase first
-  // XCD-aware tile order: workgroup b runs on XCD b % 8; give each XCD a contiguous range.
-  const int nb = gridDim.x, b = blockIdx.x;
-  const int per = nb >> 3, rem = nb & 7, xcd = b & 7, loc = b >> 3;
-  const int lid = (xcd < rem ? xcd * (per + 1) : rem * (per + 1) + (xcd - rem) * per) + loc;
+  // XCD-aware tile order: workgroup b runs on XCD b % 8; give each XCD a contiguous range of the whole tiles.
+  // Workgroups past them run one key chunk of a split tile each.
+  const int b = blockIdx.x;
+  int lid, unit = -1;
+  if (b < sp.nfull) {
+    const int nb = sp.nfull;
+    const int per = nb >> 3, rem = nb & 7, xcd = b & 7, loc = b >> 3;
+    lid = (xcd < rem ? xcd * (per + 1) : rem * (per + 1) + (xcd - rem) * per) + loc;
+  } else {
+    unit = b - sp.nfull;
+    lid = sp.nfull + unit / sp.s;
+  }
   const int h = lid / nqb, qb = lid - h * nqb;
   const int kvh = h / (p.H / p.KVH);
   const int q = qb * C::BQ + w * 32 + l32;  // this lane's query row
@@ -215,11 +238,17 @@ __global__ __launch_bounds__(NW * 64) void attention_kernel(const char *__restri
   float qsc = p.scale;
   if constexpr (C::QK8) qsc = qvalid ? fmaxf(qs[(size_t)h * p.q_rows + q] * p.scale, FLT_MIN) : 1.0f;
 
-  const char *Kh = K + (size_t)kvh * p.k_rows * RBG;
-  const char *Vh = V + (size_t)kvh * p.k_rows * DG * 2;
-  const float *ksh = C::QK8 ? ks + (size_t)kvh * p.k_rows : nullptr;
-  int kend = p.L;
-  if constexpr (CAUSAL) kend = min(p.L, qb * C::BQ + C::BQ + p.causal_off);
+  // keys of this workgroup: [key0, key0 + Lk) (a chunk of a split tile, or all L keys)
+  int key0 = 0, Lk = p.L;
+  if (unit >= 0) {
+    key0 = (unit % sp.s) * sp.cb * BK;
+    Lk = min(p.L, key0 + sp.cb * BK) - key0;
+  }
+  const char *Kh = K + ((size_t)kvh * p.k_rows + key0) * RBG;
+  const char *Vh = V + ((size_t)kvh * p.k_rows + key0) * DG * 2;
+  const float *ksh = C::QK8 ? ks + (size_t)kvh * p.k_rows + key0 : nullptr;
+  int kend = Lk;
+  if constexpr (CAUSAL) kend = min(p.L, qb * C::BQ + C::BQ + p.causal_off);  // never split
   const int nblk = kend > 0 ? (kend + BK - 1) / BK : 0;
 
   // -- staging: global -> registers -> LDS. Group g stages rows 32 g .. 32 g + 31 of every block. Buffer loads
@@ -235,7 +264,7 @@ __global__ __launch_bounds__(NW * 64) void attention_kernel(const char *__restri
   i32x4 vr[VPT];
   float ksr = 0.0f;
   auto rsrc = [&](const void *base, int blk, int row_bytes) {
-    const int rows = max(0, p.L - blk * BK);
+    const int rows = max(0, Lk - blk * BK);
     return __builtin_amdgcn_make_buffer_rsrc((void *)((const char *)base + (size_t)blk * BK * row_bytes), (short)0,
                                              rows * row_bytes, 0x00020000);
   };
@@ -416,13 +445,13 @@ __global__ __launch_bounds__(NW * 64) void attention_kernel(const char *__restri
 #pragma unroll
         for (int i = 0; i < 16; i++) x[t][i] = s[t][i];
     }
-    if (CAUSAL || kb + BK > p.L) {
+    if (CAUSAL || kb + BK > Lk) {
 #pragma unroll
       for (int t = 0; t < 2; t++)
 #pragma unroll
         for (int i = 0; i < 16; i++) {
           const int key = kb + 32 * t + 16 * (i >> 3) + 8 * hl + (i & 7);
-          bool masked = key >= p.L;
+          bool masked = key >= Lk;
           if constexpr (CAUSAL) masked = masked || key > q + p.causal_off;
           if (masked) x[t][i] = -INFINITY;
         }
@@ -493,6 +522,21 @@ __global__ __launch_bounds__(NW * 64) void attention_kernel(const char *__restri
   if (grp == 0) __syncthreads();
   if constexpr (!DUMP) {
     const float lt = l + __shfl_xor(l, 32);
+    if (unit >= 0) {
+      // partial state of this chunk, unnormalised
+      float *wrow = sp.ws + ((size_t)unit * C::BQ + (q - qb * C::BQ)) * (DG + 4);
+#pragma unroll
+      for (int db = 0; db < DG / 32; db++)
+#pragma unroll
+        for (int g = 0; g < 4; g++)
+          store4<T_F32>((char *)(wrow + db * 32 + 8 * g + 4 * hl), o[db][4 * g], o[db][4 * g + 1], o[db][4 * g + 2],
+                        o[db][4 * g + 3]);
+      if (hl == 0) {
+        wrow[DG] = m;
+        wrow[DG + 1] = lt;
+      }
+      return;
+    }
     const float inv = lt > 0.0f ? 1.0f / lt : 0.0f;
     if (qvalid) {
       constexpr int OSZ = OT == T_F32 ? 4 : 2;
@@ -510,7 +554,91 @@ __global__ __launch_bounds__(NW * 64) void attention_kernel(const char *__restri
   }
 }
 
+// Combines the chunks of the split tiles: m* = max_c m_c, w_c = 2^(m_c - m*), O = sum_c w_c O_c / sum_c w_c l_c
+// (the online-softmax merge), written like the attention epilogue. One wave per query row, 4 rows per workgroup.
+template <int DG, int OT>
+__global__ __launch_bounds__(256) void attention_merge(const float *__restrict__ ws, char *__restrict__ O, AttnParams p,
+                                                       int nqb, int nfull, int s) {
+  constexpr int BQ = NW * 32;
+  constexpr int PER = (DG + 63) / 64;  // channels per lane
+  const int lane = threadIdx.x & 63;
+  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int tr = row / BQ, r = row - tr * BQ;
+  const int tile = nfull + tr;
+  const int h = tile / nqb, qb = tile - h * nqb;
+  const int q = qb * BQ + r;
+  if (q >= p.Lq) return;
+  const float *w0 = ws + ((size_t)tr * s * BQ + r) * (DG + 4);
+  const size_t ustride = (size_t)BQ * (DG + 4);
+  float mx = -INFINITY;
+  for (int c = 0; c < s; c++) mx = fmaxf(mx, w0[c * ustride + DG]);
+  float lsum = 0.0f, acc[PER];
+#pragma unroll
+  for (int i = 0; i < PER; i++) acc[i] = 0.0f;
+  for (int c = 0; c < s; c++) {
+    const float *wr = w0 + c * ustride;
+    const float mc = wr[DG];
+    const float wt = mc == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(mc - mx);
+    lsum += wt * wr[DG + 1];
+#pragma unroll
+    for (int i = 0; i < PER; i++) {
+      const int d = lane + 64 * i;
+      if (d < DG) acc[i] += wt * wr[d];
+    }
+  }
+  const float inv = lsum > 0.0f ? 1.0f / lsum : 0.0f;
+  constexpr int OSZ = OT == T_F32 ? 4 : 2;
+  const int seq = h / p.seq_heads;
+  char *orow = O + (((size_t)seq * p.seq_rows + q) * p.o_stride + (size_t)(h - seq * p.seq_heads) * DG) * OSZ;
+#pragma unroll
+  for (int i = 0; i < PER; i++) {
+    const int d = lane + 64 * i;
+    if (d < DG) {
+      const float v = acc[i] * inv;
+      if constexpr (OT == T_F32) *(float *)(orow + d * 4) = v;
+      else if constexpr (OT == T_BF16) *(__bf16 *)(orow + d * 2) = (__bf16)v;
+      else *(_Float16 *)(orow + d * 2) = (_Float16)v;
+    }
+  }
+}
+
 int esize(int t) { return t == T_I8 ? 1 : t == T_F32 ? 4 : 2; }
+
+// CUs of the current device (the tail split sizes itself to them), cached per device.
+int cu_count() {
+  static int cache[64] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
+  if (!cache[dev]) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
+    cache[dev] = n;
+  }
+  return cache[dev];
+}
+
+// Partial-state workspace of the tail split, per stream (work on one stream is ordered, so one buffer per
+// stream is never used by two launches at once); grown on demand and kept until the process ends.
+float *split_workspace(hipStream_t stream, size_t bytes, std::string *err) {
+  static std::mutex mu;
+  static std::map<hipStream_t, std::pair<void *, size_t>> bufs;
+  std::lock_guard<std::mutex> lock(mu);
+  auto &e = bufs[stream];
+  if (e.second < bytes) {
+    if (e.first) {
+      hipStreamSynchronize(stream);  // the old buffer may still be read by queued work
+      hipFree(e.first);
+      e = {nullptr, 0};
+    }
+    void *ptr = nullptr;
+    if (hipMalloc(&ptr, bytes) != hipSuccess) {
+      *err = "attention: cannot allocate the " + std::to_string(bytes) + "-byte split workspace";
+      return nullptr;
+    }
+    e = {ptr, bytes};
+  }
+  return (float *)e.first;
+}
 
 // Host side: validation (every access the kernel makes must fall inside the
 // bound buffers) and launch.
@@ -582,11 +710,30 @@ int launch_attention(const Pipeline &pl, hipStream_t stream, const Arg *args, in
   }
   if (p.Lq == 0) return 0;
   const int nqb = (p.Lq + C::BQ - 1) / C::BQ;
-  const long nblk = (long)nqb * p.H;
-  if (nblk > 0x7fffffffL) {
+  const long ntiles = (long)nqb * p.H;
+  if (ntiles > 0x7fffffffL / 256) {
     *err = "grid too large";
     return -1;
   }
+  // Tail split (not for causal masks, whose tiles differ in length, nor for the scores dump): the R tiles of a
+  // last, partly filled round of CUs become R * s key chunks, s <= CUs / R, each at least 2 key blocks.
+  Split sp{(int)ntiles, 0, 0, nullptr};
+  const int cus = pl.ival[0] ? cu_count() : 0;
+  const int kblocks = (p.L + BK - 1) / BK;
+  if (!CAUSAL && !DUMP && cus > 0) {
+    const int R = (int)(ntiles % cus);
+    const int smax = R ? std::min(cus / R, kblocks / 2) : 0;
+    if (smax >= 2) {
+      const int cb = (kblocks + smax - 1) / smax;
+      sp.s = (kblocks + cb - 1) / cb;
+      sp.cb = cb;
+      sp.nfull = (int)ntiles - R;
+      const size_t bytes = (size_t)R * sp.s * C::BQ * (D + 4) * sizeof(float);
+      sp.ws = split_workspace(stream, bytes, err);
+      if (!sp.ws) return -1;
+    }
+  }
+  const long ngroups = sp.s ? (long)sp.nfull + (ntiles - sp.nfull) * sp.s : ntiles;
   auto kern = attention_kernel<D, QKT, VT, OT, CAUSAL, DUMP>;
   static bool attr_set = false;
   if (!attr_set) {
@@ -597,9 +744,13 @@ int launch_attention(const Pipeline &pl, hipStream_t stream, const Arg *args, in
     }
     attr_set = true;
   }
-  hipLaunchKernelGGL(kern, dim3((unsigned)nblk), dim3(C::NT), C::LDS, stream, args[0].ptr, args[1].ptr, args[2].ptr,
-                     args[3].ptr, (const float *)args[5].ptr, (const float *)args[6].ptr, p, nqb);
-  (void)pl;
+  hipLaunchKernelGGL(kern, dim3((unsigned)ngroups), dim3(C::NT), C::LDS, stream, args[0].ptr, args[1].ptr,
+                     args[2].ptr, args[3].ptr, (const float *)args[5].ptr, (const float *)args[6].ptr, p, nqb, sp);
+  if (sp.s) {
+    const int rows = (int)(ntiles - sp.nfull) * C::BQ;
+    hipLaunchKernelGGL((attention_merge<D, OT>), dim3((unsigned)(rows / 4)), dim3(256), 0, stream, sp.ws, args[3].ptr,
+                       p, nqb, sp.nfull, sp.s);
+  }
   return 0;
 }
 
@@ -642,6 +793,8 @@ int type_of(const std::string &s) {
 // V, and of Q and K without QK8; the reference's inputs are half). The
 // reference's tuning macros WM, BK, KPAD, DB, PVORDER, VX, SLACK are accepted
 // as integers and do not change the gfx950 kernel (its tiles are its own).
+// SPLIT (this build's, default 1): allow the tail split of a partly filled
+// last round of workgroups; SPLIT=0 runs every tile whole.
 bool make_attention(const std::string &fn, const Macros &m, Pipeline *pl, std::string *err) {
   const bool dump = fn == "attention_scores";
   if (fn != "attention" && !dump) {
@@ -654,9 +807,11 @@ bool make_attention(const std::string &fn, const Macros &m, Pipeline *pl, std::s
     return false;
   for (const char *k : {"WM", "BK", "KPAD", "DB", "PVORDER", "VX", "SLACK", "TG"})
     if (!macro_int(m, k, 0, &dummy, err)) return false;
+  int split;
+  if (!macro_int(m, "SPLIT", 1, &split, err)) return false;
   for (auto &kv : m) {
     static const char *known[] = {"HD", "QK8", "CAUSAL", "O_T", "IN_T", "WM", "BK", "KPAD", "DB", "PVORDER", "VX",
-                                  "SLACK", "TG"};
+                                  "SLACK", "TG", "SPLIT"};
     bool ok = false;
     for (const char *k : known) ok = ok || kv.first == k;
     if (!ok) {
@@ -681,6 +836,7 @@ bool make_attention(const std::string &fn, const Macros &m, Pipeline *pl, std::s
   else f = dump ? pick_types<64, true>(qkt, it, ot, causal) : pick_types<64, false>(qkt, it, ot, causal);
   pl->launch = f;
   pl->threads = NW * 64;
+  pl->ival[0] = split != 0;
   return true;
 }
 

@@ -398,3 +398,36 @@ def test_te_n_valid_split_dispatch(gpu):
     assert np.abs(got[:n_valid] - ref_a).max() < 5e-3
     assert np.abs(got[n_valid:T] - ref_b).max() < 5e-3
     assert (got[T:] == 0).all()
+
+
+@pytest.mark.parametrize("q8_path", [False, True])
+def test_tail_split_matches_whole_tiles(gpu, q8_path):
+    """The last, partly filled round of workgroups is cut along the keys and merged (online-softmax merge of
+    per-chunk O, m, l). Same inputs with SPLIT=0 (every tile whole): outputs agree to rounding, and both meet
+    the tolerance against float64. Here 2 heads x 2 query blocks = 4 tiles on 256 CUs: every tile is split."""
+    rng = np.random.default_rng(35)
+    H, Lq, L, D = 2, 300, 1037, 128
+    if q8_path:
+        qi, qs = q8(rng.standard_normal((H, Lq, D)).astype(np.float32))
+        ki, ks = q8(rng.standard_normal((H, L, D)).astype(np.float32))
+        q, k, extra = qi, ki, dict(q_scale=padded(gpu, qs, 512, "f32"), k_scale=padded(gpu, ks, 1056, "f32"))
+        qdt, ref_q, ref_k = "i8", qi * qs[..., None].astype(np.float64), ki * ks[..., None].astype(np.float64)
+    else:
+        q = to_bf16(rng.standard_normal((H, Lq, D)).astype(np.float32))
+        k = to_bf16(rng.standard_normal((H, L, D)).astype(np.float32))
+        extra, qdt, ref_q, ref_k = {}, "bf16", from_bf16(q), from_bf16(k)
+    v = to_bf16(rng.standard_normal((H, L, D)).astype(np.float32))
+    Q, K, V = padded(gpu, q, 512, qdt), padded(gpu, k, 1056, qdt), padded(gpu, v, 1056, "bf16")
+    outs = []
+    for split in (1, 0):
+        O = gpu.empty((512, H * D), "f32")
+        ops.attention(gpu, Q, K, V, O, Lq=Lq, L=L, H=H, KVH=H, D=D, q_rows=512, k_rows=1056, scale=D ** -0.5,
+                      SPLIT=split, **extra)
+        gpu.wait()
+        outs.append(O.numpy().astype(np.float64))
+    ref = oa.ref_attention(ref_q, ref_k, from_bf16(v), D ** -0.5)
+    for o in outs:
+        err = np.abs(o[:Lq] - ref)
+        assert err.max() < NS_MAX and err.mean() < NS_MEAN, (err.max(), err.mean())
+    assert np.abs(outs[0] - outs[1]).max() < 2e-3
+    assert (outs[0][Lq:] == 0).all()
