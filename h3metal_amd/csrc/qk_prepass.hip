@@ -148,14 +148,14 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kernel(const char *__restric
             }
           }
         }
-        // across lanes: channel c pairs with c ^ (ls * PER), stages in increasing bit order
+        // across lanes: channel c pairs with c ^ (ls * PER), stages in increasing bit order. The lower channel
+        // keeps v + o, the upper one o - v: both are fma(+-1, v, o), whose product is exact, so the one rounding
+        // is that of the sum or difference.
         auto stage = [&](auto ls_const) {
           constexpr int LS = decltype(ls_const)::value;
+          const float sg = (l32 & LS) ? -1.0f : 1.0f;
 #pragma unroll
-          for (int i = 0; i < PER; i++) {
-            const float o = xshfl<LS>(v[i]);
-            v[i] = (l32 & LS) ? o - v[i] : v[i] + o;
-          }
+          for (int i = 0; i < PER; i++) v[i] = fmaf(sg, v[i], xshfl<LS>(v[i]));
         };
         stage(std::integral_constant<int, 1>{});
         stage(std::integral_constant<int, 2>{});
@@ -176,10 +176,24 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kernel(const char *__restric
         amax = fmaxf(amax, xshfl<2>(amax));
         amax = fmaxf(amax, xshfl<1>(amax));
         const float scale = amax > 0.0f ? amax / 127.0f : 1.0f;
+        const float rs = 1.0f / scale;
         typedef typename VecOf<PER, signed char>::type CV;
         CV codes;
 #pragma unroll
-        for (int i = 0; i < PER; i++) codes[i] = (signed char)(int)rintf(v[i] / scale);
+        for (int i = 0; i < PER; i++) codes[i] = (signed char)(int)rintf(v[i] * rs);
+        // v * fl(1/scale) is within 2 ulp of the correctly rounded quotient v / scale, so its nearest integer is
+        // the quotient's unless it lies within a few ulp of a half-integer (ulp <= 2^-17 below 128): then the
+        // lanes concerned divide (rare, and exact).
+        bool near_half = false;
+#pragma unroll
+        for (int i = 0; i < PER; i++) {
+          const float y = v[i] * rs;
+          near_half |= fabsf(fabsf(y - rintf(y)) - 0.5f) < 0x1p-15f;
+        }
+        if (near_half) {
+#pragma unroll
+          for (int i = 0; i < PER; i++) codes[i] = (signed char)(int)rintf(v[i] / scale);
+        }
         *(CV *)((isq ? Qo : Ko) + hrow * HDIM + l32 * PER) = codes;
         if (l32 == rr) keep = scale;
       } else {

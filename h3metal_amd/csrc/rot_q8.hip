@@ -90,13 +90,12 @@ __global__ __launch_bounds__(256) void rot_q8_kernel(const char *__restrict__ in
           v[b][i] = a + c;
           v[b][i + s] = a - c;
         }
+    // lower column keeps v + o, upper o - v: fma(+-1, v, o), an exact product and one rounding
     auto stage = [&](auto ls_const) {
       constexpr int LS = decltype(ls_const)::value;
+      const float sg = (l32 & LS) ? -1.0f : 1.0f;
 #pragma unroll
-      for (int i = 0; i < 8; i++) {
-        const float o = xshfl<LS>(v[b][i]);
-        v[b][i] = (l32 & LS) ? o - v[b][i] : v[b][i] + o;
-      }
+      for (int i = 0; i < 8; i++) v[b][i] = fmaf(sg, v[b][i], xshfl<LS>(v[b][i]));
     };
     stage(std::integral_constant<int, 1>{});
     stage(std::integral_constant<int, 2>{});
