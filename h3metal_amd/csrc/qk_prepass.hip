@@ -19,16 +19,19 @@
 // Every floating-point step is a single IEEE-rounded operation in that order
 // (this file is compiled without FMA contraction; division and square root are
 // correctly rounded), so a float32 restatement reproduces codes and scales bit
-// for bit. The sum of squares is summed per lane, then over the 32 lanes of a
-// head with an xor butterfly (strides 16, 8, 4, 2, 1): a fixed order.
+// for bit. The sum of squares is summed per lane, then over the lanes of a
+// head with an xor butterfly (halving strides): a fixed order.
 //
-// gfx950 layout: a wave of 64 lanes handles two slots, 32 lanes per slot and
-// HDIM/32 channels per lane (lane l: channels l*PER .. l*PER + PER-1), so every
-// cross-lane step stays inside a half wave and runs on DPP / ds_swizzle (no LDS
-// memory traffic). A workgroup of 256 threads covers 8 slots of 8 consecutive
-// rows; each wave issues all 8 rows' loads before processing them, so enough
-// bytes are in flight to stream HBM, and a slot's 8 scales are stored together.
-// The kernel is HBM-bound: one read of the rows, one write of the codes / values.
+// gfx950 layout: a head's channels are spread over a group of lanes, PER
+// consecutive channels per lane: PER = 8 (16-byte loads of 16-bit rows; 16
+// lanes per head at HDIM 128) whenever the rotary pairs (c, c + rot/2) stay
+// lane-aligned (rot/2 a multiple of 8), else the reference's HDIM / 32. Every
+// cross-lane step stays inside the group and runs on DPP / ds_swizzle (no LDS
+// memory traffic). A workgroup of 256 threads covers 4 waves' groups of slots
+// of 8 consecutive rows; each wave issues all 8 rows' loads before processing
+// them, so enough bytes are in flight to stream HBM, and a slot's 8 scales are
+// stored together. The kernel is HBM-bound: one read of the rows, one write of
+// the codes / values.
 #include "h3hip_internal.h"
 
 #include <cmath>
@@ -47,18 +50,25 @@ template <> struct Elem<T_F32> { using type = float; };
 
 template <int N, typename E> struct VecOf { typedef E type __attribute__((ext_vector_type(N))); };
 
-constexpr int SLOTS_PER_WG = 8;  // (row, head) slots: two per wave, 32 lanes each
-constexpr int RPW = 8;           // rows per workgroup; each wave walks them with all their loads in flight
+constexpr int RPW = 8;  // rows per workgroup; each wave walks them with all their loads in flight
 
 template <int HDIM>
 constexpr double inv_sqrt_hdim() {
   return HDIM == 128 ? 0.0883883476483184405501055452631 : HDIM == 64 ? 0.125 : 0.1767766952966368811;
 }
 
-// Workgroup (bx, by): rows bx*RPW .. bx*RPW + RPW-1, slots by*8 .. by*8 + 7. A half wave owns one slot and
-// walks the rows; lane l32 keeps the scale of row l32 so that a slot's RPW scales (consecutive in memory within
-// a sequence) are stored together after the rows.
-template <int HDIM, int IN_T, int QK_T, int V_T, bool QKROT>
+// PER channels per lane, LPS = HDIM / PER lanes per (row, head) slot, 64 / LPS slots per wave. Workgroup
+// (bx, by): rows bx*RPW .. bx*RPW + RPW-1, slots by*SPG .. by*SPG + SPG-1 (SPG = 4 waves' slots). A lane group
+// owns one slot and walks the rows; its lane r keeps the scale of row r so that a slot's RPW scales (consecutive
+// in memory within a sequence) are stored together after the rows.
+template <int HDIM, int PER>
+struct PrepassShape {
+  static constexpr int LPS = HDIM / PER;     // lanes per slot
+  static constexpr int SPG = 4 * 64 / LPS;   // slots per workgroup
+  static_assert(LPS >= RPW && LPS <= 32 && (LPS & (LPS - 1)) == 0, "lane group");
+};
+
+template <int HDIM, int PER, int IN_T, int QK_T, int V_T, bool QKROT>
 __global__ __launch_bounds__(256) void qk_norm_rope_kernel(const char *__restrict__ in, const float *__restrict__ wq,
                                                             const float *__restrict__ wk,
                                                             const float *__restrict__ cs,
@@ -66,13 +76,16 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kernel(const char *__restric
                                                             char *__restrict__ Ko, char *__restrict__ Vo,
                                                             float *__restrict__ qsc, float *__restrict__ ksc,
                                                             QkRopeParams p) {
-  constexpr int PER = HDIM / 32;
+  using SH = PrepassShape<HDIM, PER>;
+  constexpr int LPS = SH::LPS;
   using IE = typename Elem<IN_T>::type;
   typedef typename VecOf<PER, IE>::type IV;
-  const int lane = threadIdx.x & 63, hl = lane >> 5, l32 = lane & 31, w = threadIdx.x >> 6;
-  const int slot = blockIdx.y * SLOTS_PER_WG + w * 2 + hl;
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int l32 = lane & (LPS - 1);  // lane within the slot's group
+  const int gbase = lane & ~(LPS - 1);  // first lane of the group
+  const int slot = blockIdx.y * SH::SPG + w * (64 / LPS) + lane / LPS;
   const int nslots = p.Hq + p.Hk + p.Hv;
-  if (slot >= nslots) return;  // whole half-waves only; no cross-lane step crosses halves
+  if (slot >= nslots) return;  // whole lane groups only; no cross-lane step leaves a group
   const int m0 = blockIdx.x * RPW;
   const int nr = min(RPW, p.M - m0);
 
@@ -104,8 +117,8 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kernel(const char *__restric
         float ss = v[0] * v[0];
 #pragma unroll
         for (int i = 1; i < PER; i++) ss = ss + v[i] * v[i];
-        ss = ss + xshfl<16>(ss);
-        ss = ss + xshfl<8>(ss);
+        if constexpr (LPS > 16) ss = ss + xshfl<16>(ss);
+        if constexpr (LPS > 8) ss = ss + xshfl<8>(ss);
         ss = ss + xshfl<4>(ss);
         ss = ss + xshfl<2>(ss);
         ss = ss + xshfl<1>(ss);
@@ -121,7 +134,7 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kernel(const char *__restric
         const int src_lane = l32 < lanes ? l32 + lanes : (l32 < 2 * lanes ? l32 - lanes : l32);
         float pv[PER];
 #pragma unroll
-        for (int i = 0; i < PER; i++) pv[i] = __shfl(v[i], (lane & 32) + src_lane);
+        for (int i = 0; i < PER; i++) pv[i] = __shfl(v[i], gbase + src_lane);
         if (l32 < 2 * lanes) {
           const bool first = l32 < lanes;
           const int base = (first ? l32 : l32 - lanes) * PER;  // pair index of v[0]
@@ -160,8 +173,8 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kernel(const char *__restric
         stage(std::integral_constant<int, 1>{});
         stage(std::integral_constant<int, 2>{});
         stage(std::integral_constant<int, 4>{});
-        stage(std::integral_constant<int, 8>{});
-        stage(std::integral_constant<int, 16>{});
+        if constexpr (LPS > 8) stage(std::integral_constant<int, 8>{});
+        if constexpr (LPS > 16) stage(std::integral_constant<int, 16>{});
         constexpr float rn = (float)inv_sqrt_hdim<HDIM>();
 #pragma unroll
         for (int i = 0; i < PER; i++) v[i] *= rn;
@@ -170,8 +183,8 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kernel(const char *__restric
         float amax = 0.0f;
 #pragma unroll
         for (int i = 0; i < PER; i++) amax = fmaxf(amax, fabsf(v[i]));
-        amax = fmaxf(amax, xshfl<16>(amax));
-        amax = fmaxf(amax, xshfl<8>(amax));
+        if constexpr (LPS > 16) amax = fmaxf(amax, xshfl<16>(amax));
+        if constexpr (LPS > 8) amax = fmaxf(amax, xshfl<8>(amax));
         amax = fmaxf(amax, xshfl<4>(amax));
         amax = fmaxf(amax, xshfl<2>(amax));
         amax = fmaxf(amax, xshfl<1>(amax));
@@ -292,11 +305,19 @@ int launch_qk(const Pipeline &pl, hipStream_t stream, const Arg *a, int nargs, c
     return -1;
   if (QK_T == T_I8 && (!need(9, hq * 4, "q_scale", p.Hq > 0) || !need(10, hk * 4, "k_scale", p.Hk > 0))) return -1;
   if (p.M == 0) return 0;
-  dim3 grid((unsigned)((p.M + RPW - 1) / RPW), (unsigned)((nslots + SLOTS_PER_WG - 1) / SLOTS_PER_WG));
-  hipLaunchKernelGGL((qk_norm_rope_kernel<HDIM, IN_T, QK_T, V_T, QKROT>), grid, dim3(256), 0, stream, a[0].ptr,
-                     (const float *)a[1].ptr, (const float *)a[2].ptr, (const float *)a[3].ptr,
-                     (const float *)a[4].ptr, a[5].ptr, a[6].ptr, a[7].ptr, nargs > 9 ? (float *)a[9].ptr : nullptr,
-                     nargs > 10 ? (float *)a[10].ptr : nullptr, p);
+  // 8 channels per lane (16-byte loads for 16-bit inputs) unless the rotary pairs would straddle lanes, then
+  // the reference's HDIM / 32
+  auto go = [&](auto per_const) {
+    constexpr int P = decltype(per_const)::value;
+    constexpr int SPG = PrepassShape<HDIM, P>::SPG;
+    dim3 grid((unsigned)((p.M + RPW - 1) / RPW), (unsigned)((nslots + SPG - 1) / SPG));
+    hipLaunchKernelGGL((qk_norm_rope_kernel<HDIM, P, IN_T, QK_T, V_T, QKROT>), grid, dim3(256), 0, stream, a[0].ptr,
+                       (const float *)a[1].ptr, (const float *)a[2].ptr, (const float *)a[3].ptr,
+                       (const float *)a[4].ptr, a[5].ptr, a[6].ptr, a[7].ptr,
+                       nargs > 9 ? (float *)a[9].ptr : nullptr, nargs > 10 ? (float *)a[10].ptr : nullptr, p);
+  };
+  if ((p.rot / 2) % 8 == 0) go(std::integral_constant<int, 8>{});
+  else go(std::integral_constant<int, HDIM / 32>{});
   return 0;
 }
 

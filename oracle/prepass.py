@@ -7,8 +7,9 @@ launcher h3metal/ops.py:225-239) step by step, every step one IEEE-rounded
 float32 numpy operation, in the order the gfx950 kernel performs it:
 
   load          float(in)                                         ops.metal:385-389
-  RMS norm      ss = per-lane running sum of v*v (4 channels/lane),
-                then xor butterfly over 32 lanes (16, 8, 4, 2, 1);
+  RMS norm      ss = per-lane running sum of v*v (8 channels/lane when
+                rot/2 is a multiple of 8, else hd/32), then an xor
+                butterfly over the slot's lanes (halving strides);
                 v = (v * (1 / sqrt(ss / HDIM + eps))) * w          ops.metal:394-402
   RoPE          v_c c_c - v_{c+h} s_c ; v_{c+h} c_c + v_c s_c      ops.metal:403-419
   signs         v_c = -v_c if popcount(c * 0x2545F491) is odd       ops.metal:424-428
@@ -75,18 +76,27 @@ def quant_i8(v: np.ndarray):
     return codes, scale
 
 
-def rms_norm_f32(v: np.ndarray, w: np.ndarray, eps: float) -> np.ndarray:
-    """RMS norm in the gfx950 kernel's order (per-lane partial sums, then an xor butterfly over 32 lanes)."""
+def lanes_per_slot(hd: int, rot: int) -> int:
+    """The gfx950 kernel's lane group per (row, head): 8 channels per lane (hd/8 lanes) when the rotary pairs
+    (c, c + rot/2) stay lane-aligned, i.e. rot/2 is a multiple of 8; else 32 lanes (hd/32 channels each)."""
+    return hd // 8 if (rot // 2) % 8 == 0 else 32
+
+
+def rms_norm_f32(v: np.ndarray, w: np.ndarray, eps: float, lanes: int = 32) -> np.ndarray:
+    """RMS norm in the gfx950 kernel's order: per-lane partial sums over hd/lanes consecutive channels, then an
+    xor butterfly over the `lanes` lanes (strides lanes/2 .. 1)."""
     v = v.astype(F32)
     hd = v.shape[-1]
-    per = hd // 32
-    lanes = v.reshape(v.shape[:-1] + (32, per))
-    ss = lanes[..., 0] * lanes[..., 0]
+    per = hd // lanes
+    grp = v.reshape(v.shape[:-1] + (lanes, per))
+    ss = grp[..., 0] * grp[..., 0]
     for i in range(1, per):
-        ss = ss + lanes[..., i] * lanes[..., i]
-    idx = np.arange(32)
-    for s in (16, 8, 4, 2, 1):
+        ss = ss + grp[..., i] * grp[..., i]
+    idx = np.arange(lanes)
+    s = lanes // 2
+    while s >= 1:
         ss = ss + ss[..., idx ^ s]
+        s //= 2
     tot = ss[..., 0]
     inv = F32(1) / np.sqrt(tot / F32(hd) + F32(eps))
     return (v * inv[..., None]) * w.astype(F32)
@@ -120,7 +130,7 @@ def qk_norm_rope(x: np.ndarray, *, Hq: int, Hk: int, Hv: int, hd: int, out_rows:
 
     def prep(v, w):
         if norm:
-            v = rms_norm_f32(v, w, eps)
+            v = rms_norm_f32(v, w, eps, lanes_per_slot(hd, rot))
         if rot:
             v = rope_f32(v, cs[r][:, None, :], sn[r][:, None, :], rot)
         if q8 and qk_rot:

@@ -97,6 +97,26 @@ def test_int8_norm_rope_rotation_bit_exact(gpu):
         assert np.array_equal(got[n].view(np.uint32), want[n].view(np.uint32)), n
 
 
+@pytest.mark.parametrize("hd,rot", [(128, 40), (64, 24), (64, 32), (128, 128)])
+def test_norm_rope_both_lane_layouts_bit_exact(gpu, hd, rot):
+    """8 channels per lane when rot/2 is a multiple of 8, else hd/32 per lane (the rotary pairs must stay
+    lane-aligned): both layouts against the oracle, whose norm sum follows the same lane order."""
+    rng = np.random.default_rng(hd + rot)
+    M, H = 37, 3
+    x = to_bf16((rng.standard_normal((M, 3 * H * hd)) * 2).astype(np.float32))
+    wq, wk = rng.uniform(0.5, 1.5, (2, hd)).astype(np.float32)
+    ang = rng.uniform(0, 6.28, (M, rot // 2))
+    cs, sn = np.cos(ang).astype(np.float32), np.sin(ang).astype(np.float32)
+    got = run_prepass(gpu, x, "bf16", M=M, Hq=H, Hk=H, Hv=H, hd=hd, out_rows=64, rot=rot, norm=True, eps=1e-6,
+                      wq=wq, wk=wk, cs=cs, sn=sn)
+    want = op.qk_norm_rope(from_bf16(x), Hq=H, Hk=H, Hv=H, hd=hd, out_rows=64, rot=rot, eps=1e-6, norm=True,
+                           wq=wq, wk=wk, cs=cs, sn=sn, q8=True, qk_rot=True)
+    for n in ("Q", "K"):
+        assert np.array_equal(got[n], want[n]), n
+    for n in ("qs", "ks"):
+        assert np.array_equal(got[n].view(np.uint32), want[n].view(np.uint32)), n
+
+
 def test_half_outputs_like_reference_test_qk(gpu):
     """tests/test_ops.py::test_qk (:80-111): M=21, 56 heads each, hd=128, rot=96, norm, half outputs, against a
     float64 computation with the reference's tolerance; and exactly against the float32 oracle."""
