@@ -7,7 +7,8 @@ A step is one attention call over the whole workload (all heads, all query rows)
 HBM. The default workload is BASELINE config 4: B=1, H=32, D=128, S=16896 (512 text + 16384 image rows), Q/K bf16
 ~N(0,1) with 4 of 128 channels per head x20, rotated and quantised to int8 by the fused pre-pass (timed
 separately, reported under "prepass"), V bf16 ~N(0,1), int8 QK^T + bf16 P V. The attention output's consumer,
-rot_q8 (256-block Hadamard + per-row int8 of O), is timed on the call's own output and reported under "rot_q8". FLOPs follow the reference's
+rot_q8 (256-block Hadamard + per-row int8 of O), is timed on the call's own output and reported under "rot_q8";
+the int8 projections around attention (qkv, output) at the config's S and H*D under "gemm_q8". FLOPs follow the reference's
 convention 4*H*Sq*Sk_valid*D (bench/attn_bench.py:27). The timed region is bracketed by stream
 synchronisations; GPU time comes from HIP events on the library's stream (h3_wait), per-launch durations from
 per-dispatch event pairs (profile mode). One JSON line is printed.
@@ -220,6 +221,32 @@ def main():
     rbytes = S * H * D * 2 + S * H * D + S * 4
     out["rot_q8"] = {"ms": round(rt * 1e3, 4), "bytes": rbytes, "GB/s": round(rbytes / rt / 1e9, 1),
                      "frac_hbm": round(rbytes / rt / HBM_PEAK, 4), "traffic": traffic("rot_q8_kernel")}
+    # the int8 projections around attention (h3metal/dit.py:200-215): qkv = A [S][H*D] x W^T [3*H*D] (bf16 out) and
+    # the output projection added into the float residual stream (epi 1); random int8 codes and scales
+    dm = H * D
+    grng = np.random.default_rng(1)
+    A8 = gpu.upload(grng.integers(-127, 128, size=(S, dm), dtype=np.int8))
+    SA = gpu.upload(grng.uniform(1e-3, 1e-2, S).astype(np.float32))
+    wq = ops.QWeight("q8", gpu.upload(grng.integers(-127, 128, size=(3 * dm, dm), dtype=np.int8)),
+                     gpu.upload(grng.uniform(1e-3, 1e-2, 3 * dm).astype(np.float32)), 3 * dm, dm)
+    wo = ops.QWeight("q8", gpu.upload(grng.integers(-127, 128, size=(dm, dm), dtype=np.int8)),
+                     gpu.upload(grng.uniform(1e-3, 1e-2, dm).astype(np.float32)), dm, dm)
+    QKV, X = gpu.empty((S, 3 * dm), "bf16"), gpu.empty((S, dm), "f32")
+    RT, GT = gpu.empty((S,), "u8"), gpu.upload(np.ones((1, dm), np.float32))
+    gl = {}
+    for name, fn, n_out in (("qkv", lambda: ops.gemm(gpu, A8, wq, QKV, S, sa=SA), 3 * dm),
+                            ("out", lambda: ops.gemm(gpu, A8, wo, X, S, sa=SA, epi=1, rtype=RT, gate=GT), dm)):
+        fn()
+        gpu.profile(True)
+        for _ in range(args.steps):
+            fn()
+        gpu.wait()
+        gt = float(np.mean([t for _, t in gpu.profile_take()]))
+        gpu.profile(False)
+        ops_n = 2.0 * S * n_out * dm
+        gl[name] = {"M": S, "N": n_out, "K": dm, "ms": round(gt * 1e3, 4), "TOPS": round(ops_n / gt / 1e12, 1),
+                    "frac_int8_peak": round(ops_n / gt / PEAK["int8"], 4)}
+    out["gemm_q8"] = gl
     if not args.no_cpu:
         out["cpu_baseline"] = cpu_baseline(args.config, L, args.cpu_budget)
     gpu.close()

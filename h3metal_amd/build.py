@@ -6,7 +6,7 @@ Each source compiles to an object in h3metal_amd/_build/ in parallel, then one
 shared library is linked next to this file, where gpu.py loads it. Flags:
   * --offload-arch=gfx950 only (CDNA4; no other targets),
   * packed fp32 instructions disabled (-target-feature -packed-fp32-ops),
-  * the row kernels (pre-pass, rot_q8) without FMA contraction, so their
+  * the row kernels (pre-pass, rot_q8) and the GEMM epilogue without FMA contraction, so their
     float32 steps are the separately rounded operations a CPU restatement
     reproduces bit for bit.
 """
@@ -29,8 +29,9 @@ COMMON = ["--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC", "-Wall", "-Wno-
 PER_FILE = {
     "qk_prepass.hip": ["-ffp-contract=off"],
     "rot_q8.hip": ["-ffp-contract=off"],
+    "gemm.hip": ["-ffp-contract=off"],
 }
-SOURCES = ["capi.hip", "attention.hip", "qk_prepass.hip", "rot_q8.hip"]
+SOURCES = ["capi.hip", "attention.hip", "qk_prepass.hip", "rot_q8.hip", "gemm.hip"]
 
 
 def hipcc() -> str:

@@ -263,9 +263,10 @@ void *h3_pipeline(h3_ctx *ctx, const char *file, const char *fn, const char *mac
   bool ok;
   if (mod == "attention") ok = h3::make_attention(fn, m, pl.get(), &err);
   else if (mod == "ops") ok = h3::make_ops(fn, m, pl.get(), &err);
+  else if (mod == "gemm") ok = h3::make_gemm(fn, m, pl.get(), &err);
   else {
     ok = false;
-    err = "unknown kernel module '" + std::string(file) + "' (have: attention, ops)";
+    err = "unknown kernel module '" + std::string(file) + "' (have: attention, ops, gemm)";
   }
   if (!ok) {
     set_error(key + ": " + err);

@@ -5,6 +5,7 @@
 //   AttnParams   <- kernels/params.h:41-53, packed by h3metal/ops.py:187-188 ("7if3i")
 //   QkRopeParams <- kernels/ops.metal:344-349, packed by h3metal/ops.py:237 ("8ifi")
 //   RotQParams   <- kernels/params.h:25-29, packed by h3metal/ops.py:221 ("4i")
+//   GemmParams   <- kernels/params.h:7-16, packed by h3metal/ops.py:165-166 ("8i")
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -44,6 +45,18 @@ struct RotQParams {
 };
 static_assert(sizeof(RotQParams) == 16, "RotQParams must match struct.pack('<4i')");
 
+struct GemmParams {
+  int M;         // rows of A and C (the launcher passes them padded to its tile height)
+  int N;         // output features
+  int K;         // input features
+  int a_stride;  // elements between rows of A
+  int c_stride;  // elements between rows of C (or of the residual X)
+  int w_stride;  // elements between rows of W
+  int groups;    // K / G for group-wise scales (unused by the int8 format)
+  int g_stride;  // elements between rows of the gate table
+};
+static_assert(sizeof(GemmParams) == 32, "GemmParams must match struct.pack('<8i')");
+
 using Macros = std::map<std::string, std::string>;
 
 // One bound buffer argument as the launchers see it: a device address and the
@@ -69,6 +82,7 @@ struct Pipeline {
 bool make_attention(const std::string &fn, const Macros &m, Pipeline *pl, std::string *err);
 bool make_ops(const std::string &fn, const Macros &m, Pipeline *pl, std::string *err);
 bool make_rot_q8(const Macros &m, Pipeline *pl, std::string *err);  // module "ops", function "rot_q8"
+bool make_gemm(const std::string &fn, const Macros &m, Pipeline *pl, std::string *err);
 
 // Wave64 lane exchanges inside a 32-lane half wave, shared by the row kernels: the value of lane (lane ^ S).
 // DPP for S = 1, 2 (quad_perm), ds_swizzle's xor mode (no LDS memory access) for S = 4, 8, 16.

@@ -7,6 +7,7 @@ return value (None; results are valid after `gpu.wait()`):
   attention     <- h3metal/ops.py:177-191
   qk_norm_rope  <- h3metal/ops.py:225-239
   rot_q8        <- h3metal/ops.py:214-222 (the consumer of the attention output, h3metal/dit.py:209)
+  QWeight, gemm <- h3metal/ops.py:19-34, 124-174 (the int8 projections around attention; weight format q8)
   pad_rows      <- h3metal/ops.py:116-117
 
 Element types come from the tensors, as in the reference (`OUT_DT`,
@@ -17,9 +18,12 @@ specialisations.
 
 from __future__ import annotations
 
+from dataclasses import dataclass, replace
+
 from .gpu import Gpu, Tensor, pack
 
 OUT_DT = {"f16": "half", "bf16": "bfloat", "f32": "float"}
+FMT_ID = {"q8": 1, "q4": 2, "q4g": 3, "f16": 4, "bf16": 5, "h8": 6, "h4": 7, "h4g": 8}  # h3metal/ops.py:15
 LOG2E = 1.4426950408889634
 
 
@@ -107,3 +111,59 @@ def rot_q8(gpu: Gpu, x: Tensor, out: Tensor, sa: Tensor | None, M: int, D: int, 
     k = gpu.kernel("ops", "rot_q8", NSG=nsg, MAXB=maxb, IN_T=OUT_DT[x.dtype], OUT_HR=int(out_hr))
     params = pack("4i", M, D, x_stride or (2 * D if swiglu else D), 1 if swiglu else 0)
     gpu.launch(k, None, None, [x, out, sa], params)
+
+
+@dataclass
+class QWeight:
+    """A linear layer's weight on the GPU: W[N][K] in one of the reference's formats (h3metal/ops.py:19-34).
+    This build runs the int8 format "q8" (int8 codes W[N][K] row-major, one float scale per output row sw[N])."""
+    fmt: str
+    w: Tensor
+    sw: Tensor | None
+    N: int
+    K: int
+    G: int = 128
+    bias: Tensor | None = None
+    ws: int | None = None  # row stride of the codes in elements, when it differs from K (a slice of K)
+    low: object | None = None  # a low-rank term (LoRA): not built here
+
+    @property
+    def w_stride(self) -> int:
+        return self.ws or self.K
+
+
+def gemm(gpu: Gpu, a: Tensor, wt: QWeight, out: Tensor, M: int, *, sa: Tensor | None = None, epi: int = 0,
+         rtype: Tensor | None = None, gate: Tensor | None = None, g_stride: int = 0, c_stride: int | None = None,
+         a_stride: int | None = None, tile=(64, 128, 4), swz: int = 1, ksplit: int = 1, _low=None):
+    """out = A x W^T (epi 0), or out += gate[rtype] * (A x W^T) (epi 1, out float), with A int8 [M][K] and its
+    row scales sa, W a q8 QWeight: v[m][n] = sa[m] * sw[n] * (a_m . w_n) (+ bias[n]).
+
+    ksplit: accumulate over that many consecutive slices of K in separate dispatches (epi 1 only), as the
+    reference does. tile / swz are the Metal kernel's tile choices: checked as the reference checks them (the
+    tile width must divide N) and otherwise unused (the gfx950 kernel uses 256 x 256 tiles and covers any N)."""
+    if wt.fmt != "q8":
+        raise NotImplementedError(f"gemm: weight format {wt.fmt!r} is not built (only q8)")
+    if wt.low is not None or _low is not None:
+        raise NotImplementedError("gemm: low-rank (LoRA) terms are not built")
+    if ksplit > 1:
+        if epi != 1 or wt.K % (ksplit * 256):
+            raise ValueError(f"cannot split K of a {wt.fmt} product (epi {epi}, K {wt.K}) {ksplit} ways")
+        kp = wt.K // ksplit
+        for i in range(ksplit):
+            part = replace(wt, w=wt.w.view((wt.N, kp), offset_elems=i * kp), K=kp, ws=wt.w_stride,
+                           bias=wt.bias if i == 0 else None)
+            gemm(gpu, a.view((a.shape[0], kp), offset_elems=i * kp), part, out, M, sa=sa, epi=1, rtype=rtype,
+                 gate=gate, g_stride=g_stride, c_stride=c_stride, a_stride=a_stride or wt.K, tile=tile, swz=swz)
+        return
+    tm, tn, nsg = tile
+    if wt.N % tn:
+        raise ValueError(f"gemm tile {tile}: {tn} columns do not divide the product's {wt.N}")
+    if sa is None:
+        raise ValueError("gemm: int8 activations need their row scales sa")
+    out_t = OUT_DT[out.dtype] if epi == 0 else "float"
+    k = gpu.kernel("gemm", "gemm", WFMT=FMT_ID[wt.fmt], EPI=epi, OUT_T=out_t, TM=tm, TN=tn, NSG=nsg, G=wt.G,
+                   HAS_BIAS=int(wt.bias is not None), SWZ=swz)
+    m_pad = (M + tm - 1) // tm * tm
+    params = pack("8i", m_pad, wt.N, wt.K, a_stride or wt.K, c_stride or wt.N, wt.w_stride, wt.K // wt.G,
+                  g_stride or wt.N)
+    gpu.launch(k, None, None, [a, wt.w, wt.sw, sa, out, wt.bias, rtype, gate], params, params_index=8)

@@ -67,7 +67,7 @@ void *h3_buffer_device(void *buf);
 
 // Looks up kernel `fn` of module `file` specialised by macros "NAME=value;...".
 // Modules: "attention" (fn "attention", "attention_scores") and "ops" (fn
-// "qk_norm_rope", "rot_q8"); the reference's "attention.metal"/"ops.metal" names are also
+// "qk_norm_rope", "rot_q8") and "gemm" (fn "gemm"); the reference's "attention.metal"/"ops.metal" names are also
 // accepted. NULL (with h3_last_error) for an unknown kernel or an unsupported
 // specialisation. The handle is owned by the context. Reference: src/capi.h:54-57.
 void *h3_pipeline(h3_ctx *ctx, const char *file, const char *fn, const char *macros);

@@ -10,6 +10,8 @@ missing.
   oracle.rot_q8     float32 op-by-op restatement of rot_q8, the row rotation +
                     int8 that consumes the attention output
                     (reference kernels/ops.metal:272-334)
+  oracle.gemm       the int8 projection product (reference kernels/gemm.metal,
+                    weight format q8): exact integer product, float32 epilogue
   oracle.attention  float64 softmax attention (reference tests/test_attention.py:9-21)
                     and exact integer scores
   oracle.bf16       bf16 <-> float32 conversions (round to nearest even)

@@ -1,0 +1,45 @@
+"""Restatement of the int8 projection product gemm (weight format q8).
+
+Test infrastructure only (see oracle/__init__.py).
+
+Follows the reference kernel kernels/gemm.metal (WFMT 1: :1-40 formats, :118-261 product and epilogue;
+parameters kernels/params.h:7-16; launcher h3metal/ops.py:124-174):
+
+  acc[m][n] = sum_k a[m][k] * w[n][k]               exact integer product (int64 here)
+  v         = float(acc) * sa[m] * sw[n]             float32, left to right   gemm.metal:237-238
+  v        += bias[n]                                 (HAS_BIAS)               gemm.metal:249-251
+  EPI 0     out = OUT_T(v)                                                     gemm.metal:255-256
+  EPI 1     x  += gate[rtype[m]][n] * v              (x float32)              gemm.metal:257-259
+
+Pinning status: the integer product is exact (checked against brute-force Python integer sums); the float
+epilogue is one rounding per step in this order, checked against float64 closed forms within float32 rounding
+and on hand-made values where every step is exact.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+
+F32 = np.float32
+
+
+def int_product(a: np.ndarray, w: np.ndarray) -> np.ndarray:
+    """Exact a @ w^T of int8 codes, a [M][K], w [N][K] -> int64 [M][N]. Computed in float64, which is exact
+    while |acc| < 2^53 (K * 127^2 < 2^53 for any K below 5e11)."""
+    acc = a.astype(np.float64) @ w.astype(np.float64).T
+    return acc.astype(np.int64)
+
+
+def epilogue(acc: np.ndarray, sa: np.ndarray, sw: np.ndarray, bias: np.ndarray | None = None) -> np.ndarray:
+    """float32 v = float(acc) * sa[m] * sw[n] (+ bias[n]), one rounding per operation, in the reference's order."""
+    v = acc.astype(F32) * sa.astype(F32)[:, None]
+    v = (v * sw.astype(F32)[None, :]).astype(F32)
+    if bias is not None:
+        v = (v + bias.astype(F32)[None, :]).astype(F32)
+    return v
+
+
+def residual(x: np.ndarray, v: np.ndarray, gate: np.ndarray, rtype: np.ndarray) -> np.ndarray:
+    """EPI 1: x + gate[rtype[m]][n] * v in float32 (the product rounded, then the sum)."""
+    g = gate.astype(F32)[rtype.astype(np.int64)]
+    return (x.astype(F32) + (g * v).astype(F32)).astype(F32)

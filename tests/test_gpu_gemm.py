@@ -1,0 +1,152 @@
+"""The int8 projection product (ops.gemm, weight format q8; reference kernels/gemm.metal, h3metal/ops.py:124-174)
+against the oracle: int32 products exact and the float32 epilogue bit for bit (f32 outputs and the residual
+form), 16-bit outputs equal to the rounded oracle; the reference's own tolerance checks (tests/test_gemm.py:20-84)
+on its shapes, K split over dispatches, partial tiles, and the config-4 projection shapes on sampled rows."""
+
+import numpy as np
+import pytest
+
+from h3metal_amd import ops
+from h3metal_amd.gpu import GpuError
+from oracle import gemm as og
+from oracle.bf16 import from_bf16, to_bf16
+
+pytestmark = pytest.mark.gpu
+
+
+def make(rng, M, N, K, m_pad=None, bias=False):
+    m_pad = m_pad or M
+    a = rng.integers(-127, 128, size=(m_pad, K), dtype=np.int8)
+    sa = rng.uniform(0.001, 0.01, size=m_pad).astype(np.float32)
+    q = rng.integers(-127, 128, size=(N, K), dtype=np.int8)
+    sw = rng.uniform(0.001, 0.01, size=N).astype(np.float32)
+    b = rng.standard_normal(N).astype(np.float32) if bias else None
+    return a, sa, q, sw, b
+
+
+def run(gpu, a, sa, q, sw, b, M, out_dtype="f32", tile=(64, 128, 4)):
+    N, K = q.shape
+    print(f"[gemm] M={M} N={N} K={K} out={out_dtype} bias={b is not None}", flush=True)
+    wt = ops.QWeight("q8", gpu.upload(q), gpu.upload(sw), N, K, bias=gpu.upload(b) if b is not None else None)
+    m_pad = (M + tile[0] - 1) // tile[0] * tile[0]
+    A = gpu.upload(np.pad(a, ((0, max(0, m_pad - a.shape[0])), (0, 0))))
+    SA = gpu.upload(np.pad(sa, (0, max(0, m_pad - sa.shape[0]))))
+    out = gpu.empty((m_pad, N), out_dtype)
+    ops.gemm(gpu, A, wt, out, M, sa=SA, tile=tile)
+    gpu.wait()
+    return out.numpy()[:M]
+
+
+@pytest.mark.parametrize("M,N,K,bias", [(200, 256, 512, False), (300, 640, 384, True), (64, 1024, 128, True),
+                                        (1, 256, 256, False), (513, 512, 1280, False)])
+def test_f32_outputs_bit_exact(gpu, M, N, K, bias):
+    rng = np.random.default_rng(M + N + K)
+    a, sa, q, sw, b = make(rng, M, N, K, bias=bias)
+    got = run(gpu, a, sa, q, sw, b, M)
+    want = og.epilogue(og.int_product(a[:M], q), sa[:M], sw, b)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+@pytest.mark.parametrize("out_dtype", ["f16", "bf16"])
+def test_16bit_outputs_are_the_rounded_oracle(gpu, out_dtype):
+    rng = np.random.default_rng(41)
+    M, N, K = 250, 512, 768
+    a, sa, q, sw, b = make(rng, M, N, K, bias=True)
+    got = run(gpu, a, sa, q, sw, b, M, out_dtype=out_dtype)
+    v = og.epilogue(og.int_product(a, q), sa, sw, b)
+    if out_dtype == "bf16":
+        assert np.array_equal(got, to_bf16(v))
+    else:
+        assert np.array_equal(got.view(np.uint16), v.astype(np.float16).view(np.uint16))
+
+
+def test_residual_epilogue_bit_exact_and_k_split(gpu):
+    """epi 1: X += gate[rtype] * v, exact in one dispatch; with K split over 4 dispatches (the reference's ksplit),
+    each slice's product is added in turn, which the oracle reproduces slice by slice."""
+    rng = np.random.default_rng(42)
+    M, N, K = 256, 512, 2048
+    a, sa, q, sw, b = make(rng, M, N, K, bias=True)
+    x0 = rng.standard_normal((M, N)).astype(np.float32)
+    types = rng.integers(0, 3, size=M).astype(np.uint8)
+    gates = rng.standard_normal((3, N)).astype(np.float32)
+    wt = ops.QWeight("q8", gpu.upload(q), gpu.upload(sw), N, K, bias=gpu.upload(b))
+    A, SA, RT, GT = gpu.upload(a), gpu.upload(sa), gpu.upload(types), gpu.upload(gates)
+    for ksplit in (1, 4):
+        X = gpu.upload(x0)
+        ops.gemm(gpu, A, wt, X, M, sa=SA, epi=1, rtype=RT, gate=GT, ksplit=ksplit, tile=(64, 256, 8))
+        gpu.wait()
+        want = x0
+        kp = K // ksplit
+        for i in range(ksplit):
+            sl = slice(i * kp, (i + 1) * kp)
+            v = og.epilogue(og.int_product(a[:, sl], q[:, sl]), sa, sw, b if i == 0 else None)
+            want = og.residual(want, v, gates, types)
+        assert np.array_equal(X.numpy().view(np.uint32), want.view(np.uint32)), ksplit
+
+
+@pytest.mark.parametrize("case", [dict(), dict(out_dtype="bf16"), dict(epi=1, K=2048, ksplit=4, tile=(64, 256, 8)),
+                                  dict(N=1024, tile=(32, 512, 8)), dict(epi=1, N=1024, K=2048, ksplit=4,
+                                                                          tile=(32, 512, 8))])
+def test_reference_check_cases(gpu, case):
+    """check() of tests/test_gemm.py:20-84 for the q8 format: max relative error against float64 below 2e-3
+    (1e-2 for bf16 outputs)."""
+    c = dict(M=200, N=256, K=512, epi=0, out_dtype="f16", tile=(64, 128, 4), ksplit=1)
+    c.update(case)
+    rng = np.random.default_rng(0)
+    m_pad = (c["M"] + 127) // 128 * 128
+    a = rng.integers(-127, 128, size=(m_pad, c["K"]), dtype=np.int8)
+    sa = rng.uniform(0.001, 0.01, size=m_pad).astype(np.float32)
+    q = rng.integers(-127, 128, size=(c["N"], c["K"]), dtype=np.int8)
+    sw = rng.uniform(0.001, 0.01, size=c["N"]).astype(np.float32)
+    wt = ops.QWeight("q8", gpu.upload(q), gpu.upload(sw), c["N"], c["K"])
+    ref = (a.astype(np.float64) @ q.T.astype(np.float64)) * sa[:, None] * sw[None, :]
+    A, SA = gpu.upload(a), gpu.upload(sa)
+    if c["epi"] == 0:
+        out = gpu.empty((m_pad, c["N"]), c["out_dtype"])
+        ops.gemm(gpu, A, wt, out, c["M"], sa=SA, tile=c["tile"])
+        gpu.wait()
+        got = out.numpy()[:c["M"]]
+        got = from_bf16(got).astype(np.float64) if c["out_dtype"] == "bf16" else got.astype(np.float64)
+    else:
+        x0 = rng.standard_normal((m_pad, c["N"])).astype(np.float32)
+        X = gpu.upload(x0)
+        types = rng.integers(0, 3, size=m_pad).astype(np.uint8)
+        gates = rng.standard_normal((3, c["N"])).astype(np.float32)
+        ops.gemm(gpu, A, wt, X, c["M"], sa=SA, epi=1, rtype=gpu.upload(types), gate=gpu.upload(gates),
+                 tile=c["tile"], ksplit=c["ksplit"])
+        gpu.wait()
+        got = X.numpy()[:c["M"]].astype(np.float64)
+        ref = x0.astype(np.float64) + gates[types] * ref
+    ref = ref[:c["M"]]
+    err = np.abs(got - ref).max() / (np.abs(ref).max() + 1e-12)
+    assert err < (2e-3 if c["out_dtype"] != "bf16" else 1e-2), err
+
+
+def test_config4_projection_shapes_sampled(gpu):
+    """The qkv projection of a config-4 block (M = 16896 rows, K = 4096, N = 3 * 4096, bf16 out) on the full
+    shape; 96 sampled rows against the oracle, bit for bit."""
+    rng = np.random.default_rng(43)
+    M, N, K = 16896, 12288, 4096
+    a = rng.integers(-127, 128, size=(M, K), dtype=np.int8)
+    sa = rng.uniform(0.001, 0.01, size=M).astype(np.float32)
+    q = rng.integers(-127, 128, size=(N, K), dtype=np.int8)
+    sw = rng.uniform(0.001, 0.01, size=N).astype(np.float32)
+    got = run(gpu, a, sa, q, sw, None, M, out_dtype="bf16", tile=(128, 256, 8))
+    rows = np.sort(rng.choice(M, 96, replace=False))
+    v = og.epilogue(og.int_product(a[rows], q), sa[rows], sw)
+    assert np.array_equal(got[rows], to_bf16(v))
+
+
+def test_refusals(gpu):
+    rng = np.random.default_rng(44)
+    a, sa, q, sw, _ = make(rng, 64, 256, 256)
+    wt = ops.QWeight("q8", gpu.upload(q), gpu.upload(sw), 256, 256)
+    A, SA, out = gpu.upload(a), gpu.upload(sa), gpu.empty((64, 256), "f16")
+    with pytest.raises(ValueError):  # the reference refuses tile widths that do not divide N
+        ops.gemm(gpu, A, wt, out, 64, sa=SA, tile=(32, 512, 8))
+    with pytest.raises(NotImplementedError):
+        ops.gemm(gpu, A, ops.QWeight("q4", wt.w, wt.sw, 256, 256), out, 64, sa=SA)
+    with pytest.raises(GpuError):  # K must be a multiple of 128
+        ops.gemm(gpu, A, ops.QWeight("q8", wt.w, wt.sw, 256, 200, ws=256), out, 64, sa=SA, a_stride=256)
+    with pytest.raises(GpuError):  # the output does not hold M padded rows
+        ops.gemm(gpu, A, wt, gpu.empty((32, 256), "f16"), 64, sa=SA)

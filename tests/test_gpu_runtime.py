@@ -30,7 +30,7 @@ def test_buffers_zero_filled_and_roundtrip(gpu):
 
 def test_unknown_kernel_and_macros(gpu):
     with pytest.raises(GpuError, match="unknown kernel module"):
-        gpu.kernel("gemm", "gemm")
+        gpu.kernel("nope", "gemm")
     with pytest.raises(GpuError, match="unknown function"):
         gpu.kernel("attention", "nope")
     with pytest.raises(GpuError, match="HD 80"):

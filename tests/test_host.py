@@ -123,6 +123,34 @@ def test_rot_q8_launcher_packs_reference_params():
         ops.rot_q8(g, x, out, sa, 19, 1000)
 
 
+def test_gemm_launcher_packs_reference_params():
+    """h3metal/ops.py:124-174: macros WFMT/EPI/OUT_T/HAS_BIAS (+ the tile hints), pack("8i", m_pad, N, K, a_stride,
+    c_stride, w_stride, K // G, g_stride), buffers [a, w, sw, sa, out, bias, rtype, gate], params index 8; K split
+    into consecutive slices for the residual form."""
+    g = FakeGpu()
+    a, w, sw, sa = T((256, 4096), "i8"), T((12288, 4096), "i8"), T((12288,), "f32"), T((256,), "f32")
+    out = T((256, 12288), "bf16")
+    wt = ops.QWeight("q8", w, sw, 12288, 4096)
+    ops.gemm(g, a, wt, out, 200, sa=sa)
+    (f, n, m), = g.kernels
+    assert (f, n) == ("gemm", "gemm") and m["WFMT"] == 1 and m["EPI"] == 0 and m["OUT_T"] == "bfloat"
+    assert m["HAS_BIAS"] == 0
+    (_, args, params, pi), = g.launches
+    assert pi == 8 and args[:5] == [a, w, sw, sa, out] and args[5:] == [None, None, None]
+    assert struct.unpack("<8i", params) == (256, 12288, 4096, 4096, 12288, 4096, 32, 12288)
+    g2 = FakeGpu()
+    x, rt, gate = T((256, 12288), "f32"), T((256,), "u8"), T((3, 12288), "f32")
+    ops.gemm(g2, a, wt, x, 256, sa=sa, epi=1, rtype=rt, gate=gate, ksplit=4, tile=(64, 256, 8))
+    assert len(g2.launches) == 4 and all(k[2]["EPI"] == 1 and k[2]["OUT_T"] == "float" for k in g2.kernels)
+    offs = [args[1].offset for (_, args, _, _) in g2.launches]
+    assert offs == [0, 1024, 2048, 3072]  # W slices of K / 4 columns
+    assert all(struct.unpack("<8i", p)[2:4] == (1024, 4096) for (_, _, p, _) in g2.launches)  # K slice, a_stride
+    with pytest.raises(ValueError):
+        ops.gemm(g, a, wt, out, 200, sa=sa, tile=(32, 5000, 8))
+    with pytest.raises(NotImplementedError):
+        ops.gemm(g, a, ops.QWeight("q4g", w, sw, 12288, 4096), out, 200, sa=sa)
+
+
 def test_pack_and_pad_rows():
     assert len(G.pack("7if3i", *range(7), 1.0, 0, 1, 2)) == 44  # sizeof(AttnParams), csrc/h3hip_internal.h
     assert len(G.pack("8ifi", *range(8), 1e-6, 5)) == 40         # sizeof(QkRopeParams)

@@ -308,3 +308,41 @@ def test_silu_gate_against_float64():
     v, g = x[:, :256].astype(np.float64), x[:, 256:].astype(np.float64)
     want = v * g / (1 + np.exp(-g))
     np.testing.assert_allclose(orq.silu_gated_f32(x, 256), want, rtol=3e-6, atol=1e-6)
+
+
+# -- gemm (the int8 projections) --------------------------------------------------------------------------------------
+
+def test_gemm_int_product_brute_force():
+    from oracle import gemm as og
+    rng = np.random.default_rng(9)
+    a = rng.integers(-127, 128, (5, 70), dtype=np.int8)
+    w = rng.integers(-127, 128, (3, 70), dtype=np.int8)
+    got = og.int_product(a, w)
+    for m in range(5):
+        for n in range(3):
+            assert got[m, n] == sum(int(a[m, k]) * int(w[n, k]) for k in range(70))
+    big = np.full((1, 4096), -127, np.int8)
+    assert og.int_product(big, big)[0, 0] == 4096 * 127 * 127
+
+
+def test_gemm_epilogue_order_and_exact_cases():
+    """Values where every step is exact give the exact result; random values agree with float64 within float32
+    rounding of three operations; the residual form adds gate[type] * v."""
+    from oracle import gemm as og
+    acc = np.array([[3, -5], [1024, 7]], np.int64)
+    sa, sw, bias = np.array([0.5, 2.0], np.float32), np.array([0.25, 4.0], np.float32), np.array([1.0, -1.0], np.float32)
+    v = og.epilogue(acc, sa, sw, bias)
+    assert np.array_equal(v, np.array([[3 * 0.5 * 0.25 + 1, -5 * 0.5 * 4 - 1], [1024 * 2 * 0.25 + 1, 7 * 2 * 4 - 1]],
+                                      np.float32))
+    rng = np.random.default_rng(10)
+    acc = rng.integers(-2 ** 26, 2 ** 26, (20, 30))
+    sa, sw = rng.uniform(1e-3, 1e-2, 20).astype(np.float32), rng.uniform(1e-3, 1e-2, 30).astype(np.float32)
+    want = acc.astype(np.float64) * sa[:, None].astype(np.float64) * sw[None, :].astype(np.float64)
+    np.testing.assert_allclose(og.epilogue(acc, sa, sw), want, rtol=4e-7, atol=0)
+    x = rng.standard_normal((20, 30)).astype(np.float32)
+    gate = rng.standard_normal((3, 30)).astype(np.float32)
+    rt = rng.integers(0, 3, 20).astype(np.uint8)
+    vv = og.epilogue(acc, sa, sw)
+    got = og.residual(x, vv, gate, rt)
+    np.testing.assert_allclose(got, x.astype(np.float64) + gate[rt].astype(np.float64) * vv, rtol=1e-6, atol=1e-6)
+    assert got[0, 0] == np.float32(x[0, 0] + np.float32(gate[rt[0], 0] * vv[0, 0]))
