@@ -10,12 +10,17 @@
 //
 // gfx950 design: a workgroup of 8 waves computes a 256 x 256 tile of C on v_mfma_i32_32x32x32_i8; wave
 // (wm, wn) owns rows 64 wm .. +63 and columns 128 wn .. +127 (2 x 4 MFMA tiles, 128 accumulator registers).
-// K advances in steps of 128 bytes: the A and W slices of a step (2 x 32 KB) are loaded by all 512 threads
-// with 16-byte buffer loads (rows past M or N read as zero) one step ahead into registers, then stored into
-// the other half of a double-buffered LDS area (one barrier per step). LDS rows are 128 bytes; 16-byte piece p
-// of row r is stored at p ^ ((r / 2) % 8), which makes both the staging writes and the operand reads (16 rows
-// at one piece per 16-lane pass) bank-conflict free. Workgroups are ordered so that each XCD (own L2) sweeps
-// bands of 4 row tiles across the column tiles.
+// K advances in steps of 64 bytes through 4 LDS stages of 32 KB (A rows, then W rows), filled by LDS-direct
+// 16-byte buffer loads four steps ahead (rows past M or N read as zero); one barrier per step, and the operands
+// of the next step are read from LDS while the MFMAs of the current one run. LDS rows are 64 bytes; 16-byte
+// piece p of row r sits at slot p ^ ((r / 4) % 4), which makes the operand reads (16 rows at one piece per
+// 16-lane pass) bank-conflict free. Workgroups are ordered so that each XCD (own L2) sweeps bands of 4 row
+// tiles across the column tiles.
+// Epilogues: for the plain outputs the MFMAs compute C^T (W rows as the A operand), so an accumulator lane
+// holds one row of C and 4 consecutive columns per group of 4 elements; the tile goes through LDS (float
+// outputs half a tile at a time) and leaves as 16-byte row stores. The residual form keeps C in the
+// accumulators (a lane holds one column) and reads X, writes X per wave without barriers, 128 contiguous bytes
+// of two rows per access, so one wave's epilogue overlaps the other waves' MFMAs.
 #include "h3hip_internal.h"
 
 #include <algorithm>
@@ -29,12 +34,26 @@ typedef int i32x16 __attribute__((ext_vector_type(16)));
 
 enum { T_BF16 = 1, T_F16 = 2, T_F32 = 3 };
 
-constexpr int TM = 256, TN = 256, KS = 128;  // tile rows, columns, K bytes per step
-constexpr int NWG = 8;                       // waves per workgroup
-constexpr int SW = 4;                        // row tiles per band of the tile order
-constexpr int STAGE = (TM + TN) * KS;        // LDS bytes per stage
+constexpr int TM = 256, TN = 256, KS = 64;  // tile rows, columns, K bytes per step
+constexpr int NWG = 8;                      // waves per workgroup
+constexpr int WGM = NWG / 2, WGN = 2;       // waves along the rows and the columns of the tile
+constexpr int WTM = TM / WGM, WTN = TN / WGN;  // wave tile
+constexpr int MI = WTM / 32, NJ = WTN / 32;    // 32 x 32 MFMA tiles per wave
+constexpr int NQ = TM / NWG / 16;              // 16-row LDS-direct loads per wave, operand and step
+constexpr int SW = 4;                       // row tiles per band of the tile order
+constexpr int NST = 4;                      // LDS stages
+constexpr int STAGE = (TM + TN) * KS;       // LDS bytes per stage
 
-__device__ __forceinline__ int swz(int row, int piece) { return row * KS + ((piece ^ ((row >> 1) & 7)) << 4); }
+// 16-byte piece p of LDS row r (64 bytes) sits at slot p ^ ((r / 4) % 4)
+__device__ __forceinline__ int swz(int row, int piece) { return row * KS + ((piece ^ ((row >> 2) & 3)) << 4); }
+
+// LDS-direct 16-byte buffer load: lane i's bytes land at LDS byte m0 + 16 i (offsets beyond the descriptor's
+// range read as zero). Written as assembly so that the compiler does not make every LDS read wait for all of
+// them; the kernel waits itself (vmcnt) before the barrier that publishes a stage.
+__device__ __forceinline__ void dma16(unsigned m0, int voff, __amdgpu_buffer_rsrc_t r) {
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds" ::"s"(m0), "v"(voff), "s"(r)
+               : "memory", "m0");
+}
 
 template <int OT>
 __device__ __forceinline__ void store_out(char *p, float v) {
@@ -50,11 +69,13 @@ __global__ __launch_bounds__(NWG * 64) void gemm_q8_kernel(const signed char *__
                                                            char *__restrict__ out, const float *__restrict__ bias,
                                                            const unsigned char *__restrict__ rtype,
                                                            const float *__restrict__ gate, GemmParams p, int ntm,
-                                                           int ntn, int ntypes) {
+                                                           int ntn, int ntypes, bool vec) {
   extern __shared__ __attribute__((aligned(16))) char smem[];
   const int tid = threadIdx.x, lane = tid & 63, hl = lane >> 5, l32 = lane & 31;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int wm = w >> 1, wn = w & 1;
+  const int wm = w / WGN, wn = w % WGN;
+  // accumulators hold C^T for the plain outputs (staged through LDS), C for the residual form
+  constexpr bool TR = EPI == 0;
 
   // tile order: XCD-contiguous ranges (workgroup b runs on XCD b % 8), then bands of SW row tiles
   const int nb = gridDim.x, b = blockIdx.x;
@@ -66,85 +87,251 @@ __global__ __launch_bounds__(NWG * 64) void gemm_q8_kernel(const signed char *__
   const int m0 = mt * TM, n0 = nt * TN;
 
   // staging: 4 A pieces and 4 W pieces of 16 bytes per thread and step; rows >= M (N) read as zero
-  const __amdgpu_buffer_rsrc_t ra = __builtin_amdgcn_make_buffer_rsrc(
-      (void *)(A + (size_t)m0 * p.a_stride), (short)0, max(0, min(TM, p.M - m0)) * p.a_stride, 0x00020000);
-  const __amdgpu_buffer_rsrc_t rw = __builtin_amdgcn_make_buffer_rsrc(
-      (void *)(W + (size_t)n0 * p.w_stride), (short)0, max(0, min(TN, p.N - n0)) * p.w_stride, 0x00020000);
-  i32x4 sa_r[4], sw_r[4];
-  auto load = [&](int kt) {
+  // (the record counts are wave-uniform; readfirstlane keeps the descriptors in scalar registers)
+  const int reca = __builtin_amdgcn_readfirstlane(max(0, min(TM, p.M - m0)) * p.a_stride);
+  const int recw = __builtin_amdgcn_readfirstlane(max(0, min(TN, p.N - n0)) * p.w_stride);
+  const __amdgpu_buffer_rsrc_t ra =
+      __builtin_amdgcn_make_buffer_rsrc((void *)(A + (size_t)m0 * p.a_stride), (short)0, reca, 0x00020000);
+  const __amdgpu_buffer_rsrc_t rw =
+      __builtin_amdgcn_make_buffer_rsrc((void *)(W + (size_t)n0 * p.w_stride), (short)0, recw, 0x00020000);
+  const int nk = p.K / KS;
+  // staging: a stage is 512 rows of 64 bytes (A rows 0-255, then W rows); one wave load fills 16 rows, lane l
+  // the slot l % 4 of row l / 4, with the source piece that the reader's swizzle expects there. Wave w loads
+  // rows 32 w .. 32 w + 31 of A and of W. Steps past the last read zero (offset 2^31, beyond the records).
+  const unsigned lds0 = (unsigned)(size_t)(__attribute__((address_space(3))) char *)smem;
+  const int lrow = lane >> 2, lpiece = (lane & 3) ^ ((lane >> 4) & 3);
+  int offa[NQ], offw[NQ];
 #pragma unroll
-    for (int i = 0; i < 4; i++) {
-      const int idx = tid + NWG * 64 * i, r = idx >> 3, pc = idx & 7;
-      sa_r[i] = __builtin_amdgcn_raw_buffer_load_b128(ra, r * p.a_stride + kt * KS + pc * 16, 0, 0);
-      sw_r[i] = __builtin_amdgcn_raw_buffer_load_b128(rw, r * p.w_stride + kt * KS + pc * 16, 0, 0);
-    }
-  };
-  auto store = [&](int buf) {
-    char *sA = smem + buf * STAGE, *sW = sA + TM * KS;
+  for (int q = 0; q < NQ; q++) {
+    offa[q] = (16 * (NQ * w + q) + lrow) * p.a_stride + lpiece * 16;
+    offw[q] = (16 * (NQ * w + q) + lrow) * p.w_stride + lpiece * 16;
+  }
+  auto dma = [&](int kt) __attribute__((always_inline)) {
+    const unsigned st = lds0 + (kt & (NST - 1)) * STAGE + 16 * NQ * w * KS;
+    const bool ok = kt < nk;
 #pragma unroll
-    for (int i = 0; i < 4; i++) {
-      const int idx = tid + NWG * 64 * i, r = idx >> 3, pc = idx & 7;
-      *(i32x4 *)(sA + swz(r, pc)) = sa_r[i];
-      *(i32x4 *)(sW + swz(r, pc)) = sw_r[i];
+    for (int q = 0; q < NQ; q++) {
+      dma16(st + 16 * q * KS, ok ? offa[q] + kt * KS : (int)0x80000000u, ra);
+      dma16(st + TM * KS + 16 * q * KS, ok ? offw[q] + kt * KS : (int)0x80000000u, rw);
     }
   };
 
-  i32x16 acc[2][4];
+  i32x16 acc[MI][NJ];
 #pragma unroll
-  for (int i = 0; i < 2; i++)
+  for (int i = 0; i < MI; i++)
 #pragma unroll
-    for (int j = 0; j < 4; j++)
+    for (int j = 0; j < NJ; j++)
 #pragma unroll
       for (int e = 0; e < 16; e++) acc[i][j][e] = 0;
 
-  const int nk = p.K / KS;
-  load(0);
-  store(0);
-  __syncthreads();
-  for (int kt = 0; kt < nk; kt++) {
-    if (kt + 1 < nk) load(kt + 1);
-    const char *sA = smem + (kt & 1) * STAGE, *sW = sA + TM * KS;
+  // Operands of a step: 2 A and 4 W pieces for each 32-byte half of the step's K.
+  struct Ops {
+    i32x4 a[2][MI], w[2][NJ];
+  };
+  auto read_ops = [&](Ops &o, int kt) __attribute__((always_inline)) {
+    const char *sA = smem + (kt & (NST - 1)) * STAGE, *sW = sA + TM * KS;
 #pragma unroll
     for (int c = 0; c < KS / 32; c++) {
-      i32x4 a[2], bw[4];
 #pragma unroll
-      for (int i = 0; i < 2; i++) a[i] = *(const i32x4 *)(sA + swz(64 * wm + 32 * i + l32, 2 * c + hl));
+      for (int i = 0; i < MI; i++) o.a[c][i] = *(const i32x4 *)(sA + swz(WTM * wm + 32 * i + l32, 2 * c + hl));
 #pragma unroll
-      for (int j = 0; j < 4; j++) bw[j] = *(const i32x4 *)(sW + swz(128 * wn + 32 * j + l32, 2 * c + hl));
-#pragma unroll
-      for (int i = 0; i < 2; i++)
-#pragma unroll
-        for (int j = 0; j < 4; j++) acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[i], bw[j], acc[i][j], 0, 0, 0);
+      for (int j = 0; j < NJ; j++) o.w[c][j] = *(const i32x4 *)(sW + swz(WTN * wn + 32 * j + l32, 2 * c + hl));
     }
-    if (kt + 1 < nk) store((kt + 1) & 1);
+  };
+  // Step kt: its operands are already in registers (cur). Once stage kt + 1 has landed (own loads: vmcnt;
+  // everyone's: the barrier, which also completes every wave's reads of stage kt), stage kt is refilled with
+  // step kt + 4, and the MFMAs of step kt are interleaved with the reads of step kt + 1's operands (nxt).
+  auto step = [&](int kt, const Ops &cur, Ops &nxt) __attribute__((always_inline)) {
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(4 * NQ) : "memory");
     __syncthreads();
-  }
+    dma(kt + 4);
+    read_ops(nxt, kt + 1);
+#pragma unroll
+    for (int c = 0; c < KS / 32; c++)
+#pragma unroll
+      for (int i = 0; i < MI; i++)
+#pragma unroll
+        for (int j = 0; j < NJ; j++)
+          acc[i][j] = TR ? __builtin_amdgcn_mfma_i32_32x32x32_i8(cur.w[c][j], cur.a[c][i], acc[i][j], 0, 0, 0)
+                         : __builtin_amdgcn_mfma_i32_32x32x32_i8(cur.a[c][i], cur.w[c][j], acc[i][j], 0, 0, 0);
+    constexpr int NR = 2 * (MI + NJ), NF = 2 * MI * NJ;  // LDS reads and MFMAs of a step
+#pragma unroll
+    for (int g = 0; g < NR; g++) {
+      __builtin_amdgcn_sched_group_barrier(0x008, NF / NR, 0);  // MFMAs
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);        // one LDS read
+    }
+    __builtin_amdgcn_sched_group_barrier(0x008, NF - NR * (NF / NR), 0);
+  };
 
-  // epilogue: accumulator element e of tile (i, j) is row 64 wm + 32 i + 8 (e / 4) + 4 hl + e % 4, column
-  // 128 wn + 32 j + l32
-  constexpr int OSZ = OT == T_F32 ? 4 : 2;
+  dma(0);
+  dma(1);
+  dma(2);
+  dma(3);
+  Ops o0, o1;
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(6 * NQ) : "memory");
+  __syncthreads();
+  read_ops(o0, 0);
+  for (int kt = 0; kt < nk; kt += 2) {
+    step(kt, o0, o1);
+    if (kt + 1 < nk) step(kt + 1, o1, o0);
+  }
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+
+  if constexpr (EPI == 1) {
+    // residual form: accumulator element e of tile (i, j) is C[m][n] with m = WTM wm + 32 i + 8 (e / 4) + 4 hl +
+    // e % 4 and n = WTN wn + 32 j + l32 (tile-relative), so each store writes 128 contiguous bytes of two rows.
+    // Stores are per wave, without barriers, so a wave's epilogue overlaps the other waves' MFMAs. Per-row values
+    // are loaded once (rows past M clamp to the last row and are not stored); the loads of a tile are issued
+    // before its stores.
+    auto row_of = [&](int i, int e) { return m0 + WTM * wm + 32 * i + 8 * (e >> 2) + 4 * hl + (e & 3); };
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 #pragma unroll
-  for (int j = 0; j < 4; j++) {
-    const int n = n0 + 128 * wn + 32 * j + l32;
-    if (n >= p.N) continue;
-    const float swn = sw[n];
-    const float bn = HAS_BIAS ? bias[n] : 0.0f;
-#pragma unroll
-    for (int i = 0; i < 2; i++)
+    for (int i = 0; i < MI; i++) {
+      float sam[16];
+      int goff[16];
 #pragma unroll
       for (int e = 0; e < 16; e++) {
-        const int m = m0 + 64 * wm + 32 * i + 8 * (e >> 2) + 4 * hl + (e & 3);
-        if (m >= p.M) continue;
-        float v = (float)acc[i][j][e] * sa[m] * swn;
-        if constexpr (HAS_BIAS) v += bn;
-        if constexpr (EPI == 0) {
-          store_out<OT>(out + ((size_t)m * p.c_stride + n) * OSZ, v);
-        } else {
-          float *x = (float *)out + (size_t)m * p.c_stride + n;
-          const int ty = min((int)rtype[m], ntypes - 1);  // types past the gate table's rows clamp to its last
-          *x += gate[(size_t)ty * p.g_stride + n] * v;
+        const int m = min(row_of(i, e), p.M - 1);
+        sam[e] = sa[m];
+        // row types past the gate table's rows clamp to its last
+        goff[e] = min((int)rtype[m], ntypes - 1) * p.g_stride;
+      }
+#pragma unroll
+      for (int j = 0; j < NJ; j++) {
+        const int n = n0 + WTN * wn + 32 * j + l32;
+        const bool nok = n < p.N;
+        const int nc = min(n, p.N - 1);
+        const float swn = sw[nc];
+        const float bn = HAS_BIAS ? bias[nc] : 0.0f;
+        float xv[16], gv[16];
+#pragma unroll
+        for (int e = 0; e < 16; e++) {
+          xv[e] = ((const float *)out)[(size_t)min(row_of(i, e), p.M - 1) * p.c_stride + nc];
+          gv[e] = gate[goff[e] + nc];
+        }
+#pragma unroll
+        for (int e = 0; e < 16; e++) {
+          const int m = row_of(i, e);
+          float v = (float)acc[i][j][e] * sam[e] * swn;
+          if constexpr (HAS_BIAS) v += bn;
+          if (nok && m < p.M) ((float *)out)[(size_t)m * p.c_stride + n] = xv[e] + gv[e] * v;
         }
       }
+    }
+    return;
+  }
+
+  // plain outputs: accumulator element e of tile (i, j) is C[m][n] with m = WTM wm + 32 i + l32 and
+  // n = WTN wn + 32 j + 8 (e / 4) + 4 hl + e % 4 (tile-relative). Rows past M and columns past N are not
+  // stored; their loads clamp to the last row and column.
+  constexpr int OSZ = OT == T_F32 ? 4 : 2;
+  float sam[MI];
+#pragma unroll
+  for (int i = 0; i < MI; i++) sam[i] = sa[min(m0 + WTM * wm + 32 * i + l32, p.M - 1)];
+  auto value = [&](int i, int j, int e, float swn, float bn) __attribute__((always_inline)) {
+    float v = (float)acc[i][j][e] * sam[i] * swn;
+    if constexpr (HAS_BIAS) v += bn;
+    return v;
+  };
+  auto ld4 = [&](const float *q, int n) __attribute__((always_inline)) {  // q[n .. n + 3], clamped per element
+    float4 r;
+    if (vec) {
+      r = *(const float4 *)(q + n);
+    } else {
+      r.x = q[min(n, p.N - 1)];
+      r.y = q[min(n + 1, p.N - 1)];
+      r.z = q[min(n + 2, p.N - 1)];
+      r.w = q[min(n + 3, p.N - 1)];
+    }
+    return r;
+  };
+  if constexpr (OT != T_F32) {
+    // 16-bit outputs: the tile's values into LDS (rows of 256 values, 528-byte stride), then 16-byte row stores
+    constexpr int RS = TN * 2 + 16;
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < NJ; j++)
+#pragma unroll
+      for (int q = 0; q < 4; q++) {
+        const int nl = WTN * wn + 32 * j + 8 * q + 4 * hl, n = n0 + nl;
+        const float4 s4 = ld4(sw, min(n, vec ? p.N - 4 : n));
+        float4 b4 = {0, 0, 0, 0};
+        if constexpr (HAS_BIAS) b4 = ld4(bias, min(n, vec ? p.N - 4 : n));
+        const float sv[4] = {s4.x, s4.y, s4.z, s4.w}, bv[4] = {b4.x, b4.y, b4.z, b4.w};
+#pragma unroll
+        for (int i = 0; i < MI; i++) {
+          unsigned short h[4];
+#pragma unroll
+          for (int r = 0; r < 4; r++) {
+            const float v = value(i, j, 4 * q + r, sv[r], bv[r]);
+            if constexpr (OT == T_BF16) h[r] = __builtin_bit_cast(unsigned short, (__bf16)v);
+            else h[r] = __builtin_bit_cast(unsigned short, (_Float16)v);
+          }
+          const int ml = WTM * wm + 32 * i + l32;
+          *(uint2 *)(smem + ml * RS + nl * 2) = make_uint2(h[0] | (unsigned)h[1] << 16, h[2] | (unsigned)h[3] << 16);
+        }
+      }
+    __syncthreads();
+    // 256 rows x 32 pieces of 16 bytes, 16 per thread, consecutive threads along a row
+#pragma unroll 4
+    for (int c = tid; c < TM * 32; c += NWG * 64) {
+      const int ml = c >> 5, pc = c & 31, m = m0 + ml, n = n0 + 8 * pc;
+      if (m >= p.M || n >= p.N) continue;
+      const uint4 d = *(const uint4 *)(smem + ml * RS + pc * 16);
+      char *dst = out + ((size_t)m * p.c_stride + n) * 2;
+      if (vec) {
+        *(uint4 *)dst = d;
+      } else {
+        const unsigned short *hs = (const unsigned short *)&d;
+        for (int r = 0; r < 8 && n + r < p.N; r++) ((unsigned short *)dst)[r] = hs[r];
+      }
+    }
+  } else {
+    // float outputs: half a tile at a time (128 rows of 256 values, 1040-byte stride) into LDS, then 16-byte
+    // row stores
+    constexpr int RS = TN * 4 + 16, HR = TM / 2;
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+#pragma unroll
+    for (int h = 0; h < 2; h++) {
+      __syncthreads();
+      if (WTM * wm / HR == h) {
+#pragma unroll
+        for (int j = 0; j < NJ; j++)
+#pragma unroll
+          for (int q = 0; q < 4; q++) {
+            const int nl = WTN * wn + 32 * j + 8 * q + 4 * hl, n = n0 + nl;
+            const float4 s4 = ld4(sw, min(n, vec ? p.N - 4 : n));
+            float4 b4 = {0, 0, 0, 0};
+            if constexpr (HAS_BIAS) b4 = ld4(bias, min(n, vec ? p.N - 4 : n));
+            const float sv[4] = {s4.x, s4.y, s4.z, s4.w}, bv[4] = {b4.x, b4.y, b4.z, b4.w};
+#pragma unroll
+            for (int i = 0; i < MI; i++) {
+              float o[4];
+#pragma unroll
+              for (int r = 0; r < 4; r++) o[r] = value(i, j, 4 * q + r, sv[r], bv[r]);
+              const int ml = WTM * wm + 32 * i + l32 - HR * h;
+              *(float4 *)(smem + ml * RS + nl * 4) = make_float4(o[0], o[1], o[2], o[3]);
+            }
+          }
+      }
+      __syncthreads();
+      // 128 rows x 64 pieces of 16 bytes, 16 per thread (rows ml0 + 8 k), consecutive threads along a row;
+      const int pc = tid & 63, n = n0 + 4 * pc;
+#pragma unroll 4
+      for (int ml = tid >> 6; ml < HR; ml += NWG) {
+        const int m = m0 + HR * h + ml;
+        if (m >= p.M || n >= p.N) continue;
+        const float4 o = *(const float4 *)(smem + ml * RS + pc * 16);
+        float *dst = (float *)out + (size_t)m * p.c_stride + n;
+        if (vec) {
+          *(float4 *)dst = o;
+        } else {
+          const float ov[4] = {o.x, o.y, o.z, o.w};
+          for (int r = 0; r < 4 && n + r < p.N; r++) dst[r] = ov[r];
+        }
+      }
+    }
   }
 }
 
@@ -162,7 +349,7 @@ int launch_gemm(const Pipeline &pl, hipStream_t stream, const Arg *a, int nargs,
   if (p.M < 0 || p.N < 1 || p.K < KS || p.K % KS || p.a_stride < p.K || p.w_stride < p.K || p.c_stride < p.N ||
       p.a_stride % 16 || p.w_stride % 16) {
     *err = "bad shape: M " + std::to_string(p.M) + " N " + std::to_string(p.N) + " K " + std::to_string(p.K) +
-           " (a multiple of 128) a_stride " + std::to_string(p.a_stride) + " w_stride " +
+           " (a multiple of 64) a_stride " + std::to_string(p.a_stride) + " w_stride " +
            std::to_string(p.w_stride) + " (multiples of 16) c_stride " + std::to_string(p.c_stride);
     return -1;
   }
@@ -204,22 +391,29 @@ int launch_gemm(const Pipeline &pl, hipStream_t stream, const Arg *a, int nargs,
       *err = std::string(i ? "w" : "a") + " must be 16-byte aligned";
       return -1;
     }
+  // 16-byte vector access to the output (and the column vectors) when alignment and N allow it
+  constexpr int VE = 16 / OSZ;
+  auto al16 = [](const void *q) { return (uintptr_t)q % 16 == 0; };
+  const bool vec = al16(a[4].ptr) && (p.c_stride * OSZ) % 16 == 0 && p.N % VE == 0 && al16(a[2].ptr) &&
+                   (!HAS_BIAS || al16(a[5].ptr)) && (!EPI || (al16(a[7].ptr) && p.g_stride % 4 == 0));
   const int ntm = (p.M + TM - 1) / TM, ntn = (p.N + TN - 1) / TN;
   auto kern = gemm_q8_kernel<OT, EPI, HAS_BIAS>;
+  constexpr int LDS_BYTES =
+      std::max(NST * STAGE, OT == T_F32 ? TM / 2 * (TN * 4 + 16) : TM * (TN * 2 + 16));
   static bool attr_set = false;
   if (!attr_set) {
-    hipError_t e = hipFuncSetAttribute((const void *)kern, hipFuncAttributeMaxDynamicSharedMemorySize, 2 * STAGE);
+    hipError_t e = hipFuncSetAttribute((const void *)kern, hipFuncAttributeMaxDynamicSharedMemorySize, LDS_BYTES);
     if (e != hipSuccess) {
       *err = std::string("hipFuncSetAttribute: ") + hipGetErrorString(e);
       return -1;
     }
     attr_set = true;
   }
-  hipLaunchKernelGGL(kern, dim3((unsigned)(ntm * ntn)), dim3(NWG * 64), 2 * STAGE, stream,
+  hipLaunchKernelGGL(kern, dim3((unsigned)(ntm * ntn)), dim3(NWG * 64), LDS_BYTES, stream,
                      (const signed char *)a[0].ptr, (const signed char *)a[1].ptr, (const float *)a[2].ptr,
                      (const float *)a[3].ptr, a[4].ptr, HAS_BIAS ? (const float *)a[5].ptr : nullptr,
                      EPI ? (const unsigned char *)a[6].ptr : nullptr, EPI ? (const float *)a[7].ptr : nullptr, p, ntm,
-                     ntn, ntypes);
+                     ntn, ntypes, vec);
   return 0;
 }
 

@@ -60,6 +60,43 @@ def test_16bit_outputs_are_the_rounded_oracle(gpu, out_dtype):
         assert np.array_equal(got.view(np.uint16), v.astype(np.float16).view(np.uint16))
 
 
+@pytest.mark.parametrize("N,out_dtype", [(200, "f16"), (198, "bf16"), (198, "f32"), (260, "f32")])
+def test_ragged_columns_element_path(gpu, N, out_dtype):
+    """Column counts that are not a multiple of the 16-byte vector (and partial column tiles): the kernel's
+    per-element output path, bit-exact."""
+    rng = np.random.default_rng(N)
+    M, K = 70, 192
+    a, sa, q, sw, b = make(rng, M, N, K, bias=True)
+    got = run(gpu, a, sa, q, sw, b, M, out_dtype=out_dtype, tile=(64, 2, 4))
+    v = og.epilogue(og.int_product(a[:M], q), sa[:M], sw, b)
+    if out_dtype == "f32":
+        assert np.array_equal(got.view(np.uint32), v.view(np.uint32))
+    elif out_dtype == "bf16":
+        assert np.array_equal(got, to_bf16(v))
+    else:
+        assert np.array_equal(got.view(np.uint16), v.astype(np.float16).view(np.uint16))
+
+
+def test_residual_ragged_columns_and_strided_output(gpu):
+    """epi 1 with N = 198 into a residual buffer with a wider row stride (c_stride 203): element path; the
+    columns past N are left alone."""
+    rng = np.random.default_rng(5)
+    M, N, K, CS = 128, 198, 256, 203
+    a, sa, q, sw, b = make(rng, M, N, K, bias=True)
+    x0 = rng.standard_normal((M, CS)).astype(np.float32)
+    types = rng.integers(0, 2, size=M).astype(np.uint8)
+    gates = rng.standard_normal((2, N)).astype(np.float32)
+    wt = ops.QWeight("q8", gpu.upload(q), gpu.upload(sw), N, K, bias=gpu.upload(b))
+    X = gpu.upload(x0)
+    ops.gemm(gpu, gpu.upload(a), wt, X, M, sa=gpu.upload(sa), epi=1, rtype=gpu.upload(types),
+             gate=gpu.upload(gates), c_stride=CS, tile=(64, 2, 4))
+    gpu.wait()
+    v = og.epilogue(og.int_product(a, q), sa, sw, b)
+    want = x0.copy()
+    want[:, :N] = og.residual(x0[:, :N], v, gates, types)
+    assert np.array_equal(X.numpy().view(np.uint32), want.view(np.uint32))
+
+
 def test_residual_epilogue_bit_exact_and_k_split(gpu):
     """epi 1: X += gate[rtype] * v, exact in one dispatch; with K split over 4 dispatches (the reference's ksplit),
     each slice's product is added in turn, which the oracle reproduces slice by slice."""
