@@ -34,15 +34,16 @@ typedef int i32x16 __attribute__((ext_vector_type(16)));
 
 enum { T_BF16 = 1, T_F16 = 2, T_F32 = 3 };
 
-constexpr int TM = 256, TN = 256, KS = 64;  // tile rows, columns, K bytes per step
-constexpr int NWG = 8;                      // waves per workgroup
-constexpr int WGM = NWG / 2, WGN = 2;       // waves along the rows and the columns of the tile
-constexpr int WTM = TM / WGM, WTN = TN / WGN;  // wave tile
-constexpr int MI = WTM / 32, NJ = WTN / 32;    // 32 x 32 MFMA tiles per wave
-constexpr int NQ = TM / NWG / 16;              // 16-row LDS-direct loads per wave, operand and step
-constexpr int SW = 4;                       // row tiles per band of the tile order
-constexpr int NST = 4;                      // LDS stages
-constexpr int STAGE = (TM + TN) * KS;       // LDS bytes per stage
+constexpr int TM = 256, TN = 256, KS = 64;       // tile rows, columns, K bytes per step
+constexpr int NWG = 8;                           // waves per workgroup
+constexpr int WGN = 2, WGM = NWG / WGN;          // waves along the columns and the rows of the tile
+constexpr int WTM = TM / WGM, WTN = TN / WGN;    // wave tile
+constexpr int MI = WTM / 32, NJ = WTN / 32;      // 32 x 32 MFMA tiles per wave
+constexpr int NQA = TM / NWG / 16, NQW = TN / NWG / 16;  // 16-row LDS-direct loads per wave and step
+constexpr int LPS = NQA + NQW;                   // loads per wave and step
+constexpr int SW = 4;                            // row tiles per band of the tile order
+constexpr int NST = 4;                           // LDS stages
+constexpr int STAGE = (TM + TN) * KS;            // LDS bytes per stage
 
 // 16-byte piece p of LDS row r (64 bytes) sits at slot p ^ ((r / 4) % 4)
 __device__ __forceinline__ int swz(int row, int piece) { return row * KS + ((piece ^ ((row >> 2) & 3)) << 4); }
@@ -63,7 +64,7 @@ __device__ __forceinline__ void store_out(char *p, float v) {
 }
 
 template <int OT, int EPI, bool HAS_BIAS>
-__global__ __launch_bounds__(NWG * 64) void gemm_q8_kernel(const signed char *__restrict__ A,
+__global__ __launch_bounds__(NWG * 64) __attribute__((amdgpu_waves_per_eu(2))) void gemm_q8_kernel(const signed char *__restrict__ A,
                                                            const signed char *__restrict__ W,
                                                            const float *__restrict__ sw, const float *__restrict__ sa,
                                                            char *__restrict__ out, const float *__restrict__ bias,
@@ -100,20 +101,20 @@ __global__ __launch_bounds__(NWG * 64) void gemm_q8_kernel(const signed char *__
   // rows 32 w .. 32 w + 31 of A and of W. Steps past the last read zero (offset 2^31, beyond the records).
   const unsigned lds0 = (unsigned)(size_t)(__attribute__((address_space(3))) char *)smem;
   const int lrow = lane >> 2, lpiece = (lane & 3) ^ ((lane >> 4) & 3);
-  int offa[NQ], offw[NQ];
+  int offa[NQA], offw[NQW];
 #pragma unroll
-  for (int q = 0; q < NQ; q++) {
-    offa[q] = (16 * (NQ * w + q) + lrow) * p.a_stride + lpiece * 16;
-    offw[q] = (16 * (NQ * w + q) + lrow) * p.w_stride + lpiece * 16;
-  }
+  for (int q = 0; q < NQA; q++) offa[q] = (16 * (NQA * w + q) + lrow) * p.a_stride + lpiece * 16;
+#pragma unroll
+  for (int q = 0; q < NQW; q++) offw[q] = (16 * (NQW * w + q) + lrow) * p.w_stride + lpiece * 16;
   auto dma = [&](int kt) __attribute__((always_inline)) {
-    const unsigned st = lds0 + (kt & (NST - 1)) * STAGE + 16 * NQ * w * KS;
+    const unsigned st = lds0 + ((unsigned)kt % NST) * STAGE;
     const bool ok = kt < nk;
 #pragma unroll
-    for (int q = 0; q < NQ; q++) {
-      dma16(st + 16 * q * KS, ok ? offa[q] + kt * KS : (int)0x80000000u, ra);
-      dma16(st + TM * KS + 16 * q * KS, ok ? offw[q] + kt * KS : (int)0x80000000u, rw);
-    }
+    for (int q = 0; q < NQA; q++)
+      dma16(st + (16 * (NQA * w + q)) * KS, ok ? offa[q] + kt * KS : (int)0x80000000u, ra);
+#pragma unroll
+    for (int q = 0; q < NQW; q++)
+      dma16(st + (TM + 16 * (NQW * w + q)) * KS, ok ? offw[q] + kt * KS : (int)0x80000000u, rw);
   };
 
   i32x16 acc[MI][NJ];
@@ -129,7 +130,7 @@ __global__ __launch_bounds__(NWG * 64) void gemm_q8_kernel(const signed char *__
     i32x4 a[2][MI], w[2][NJ];
   };
   auto read_ops = [&](Ops &o, int kt) __attribute__((always_inline)) {
-    const char *sA = smem + (kt & (NST - 1)) * STAGE, *sW = sA + TM * KS;
+    const char *sA = smem + ((unsigned)kt % NST) * STAGE, *sW = sA + TM * KS;
 #pragma unroll
     for (int c = 0; c < KS / 32; c++) {
 #pragma unroll
@@ -140,11 +141,11 @@ __global__ __launch_bounds__(NWG * 64) void gemm_q8_kernel(const signed char *__
   };
   // Step kt: its operands are already in registers (cur). Once stage kt + 1 has landed (own loads: vmcnt;
   // everyone's: the barrier, which also completes every wave's reads of stage kt), stage kt is refilled with
-  // step kt + 4, and the MFMAs of step kt are interleaved with the reads of step kt + 1's operands (nxt).
+  // step kt + NST, and the MFMAs of step kt are interleaved with the reads of step kt + 1's operands (nxt).
   auto step = [&](int kt, const Ops &cur, Ops &nxt) __attribute__((always_inline)) {
-    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(4 * NQ) : "memory");
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"((NST - 2) * LPS) : "memory");
     __syncthreads();
-    dma(kt + 4);
+    dma(kt + NST);
     read_ops(nxt, kt + 1);
 #pragma unroll
     for (int c = 0; c < KS / 32; c++)
@@ -163,12 +164,10 @@ __global__ __launch_bounds__(NWG * 64) void gemm_q8_kernel(const signed char *__
     __builtin_amdgcn_sched_group_barrier(0x008, NF - NR * (NF / NR), 0);
   };
 
-  dma(0);
-  dma(1);
-  dma(2);
-  dma(3);
+#pragma unroll
+  for (int s = 0; s < NST; s++) dma(s);
   Ops o0, o1;
-  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(6 * NQ) : "memory");
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"((NST - 1) * LPS) : "memory");
   __syncthreads();
   read_ops(o0, 0);
   for (int kt = 0; kt < nk; kt += 2) {
@@ -246,7 +245,8 @@ __global__ __launch_bounds__(NWG * 64) void gemm_q8_kernel(const signed char *__
     return r;
   };
   if constexpr (OT != T_F32) {
-    // 16-bit outputs: the tile's values into LDS (rows of 256 values, 528-byte stride), then 16-byte row stores
+    // 16-bit outputs: the tile's values into LDS (rows of TN values, 2 TN + 16 bytes apart), then 16-byte row
+    // stores
     constexpr int RS = TN * 2 + 16;
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
@@ -273,10 +273,11 @@ __global__ __launch_bounds__(NWG * 64) void gemm_q8_kernel(const signed char *__
         }
       }
     __syncthreads();
-    // 256 rows x 32 pieces of 16 bytes, 16 per thread, consecutive threads along a row
+    // TM rows x TN / 8 pieces of 16 bytes, consecutive threads along a row
+    constexpr int PPR = TN / 8;
 #pragma unroll 4
-    for (int c = tid; c < TM * 32; c += NWG * 64) {
-      const int ml = c >> 5, pc = c & 31, m = m0 + ml, n = n0 + 8 * pc;
+    for (int c = tid; c < TM * PPR; c += NWG * 64) {
+      const int ml = c / PPR, pc = c % PPR, m = m0 + ml, n = n0 + 8 * pc;
       if (m >= p.M || n >= p.N) continue;
       const uint4 d = *(const uint4 *)(smem + ml * RS + pc * 16);
       char *dst = out + ((size_t)m * p.c_stride + n) * 2;
@@ -288,7 +289,7 @@ __global__ __launch_bounds__(NWG * 64) void gemm_q8_kernel(const signed char *__
       }
     }
   } else {
-    // float outputs: half a tile at a time (128 rows of 256 values, 1040-byte stride) into LDS, then 16-byte
+    // float outputs: half a tile at a time (TM / 2 rows of TN values, 4 TN + 16 bytes apart) into LDS, then 16-byte
     // row stores
     constexpr int RS = TN * 4 + 16, HR = TM / 2;
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
@@ -317,9 +318,10 @@ __global__ __launch_bounds__(NWG * 64) void gemm_q8_kernel(const signed char *__
       }
       __syncthreads();
       // 128 rows x 64 pieces of 16 bytes, 16 per thread (rows ml0 + 8 k), consecutive threads along a row;
-      const int pc = tid & 63, n = n0 + 4 * pc;
+      constexpr int PPR = TN / 4;  // 16-byte pieces per row
+      const int pc = tid % PPR, n = n0 + 4 * pc;
 #pragma unroll 4
-      for (int ml = tid >> 6; ml < HR; ml += NWG) {
+      for (int ml = tid / PPR; ml < HR; ml += NWG * 64 / PPR) {
         const int m = m0 + HR * h + ml;
         if (m >= p.M || n >= p.N) continue;
         const float4 o = *(const float4 *)(smem + ml * RS + pc * 16);
