@@ -1,10 +1,10 @@
-"""Attention throughput on one MI355X: the BASELINE metric (attention TFLOP/s and % of the int8 MFMA peak at
+"""Attention throughput on one MI355X: the headline metric (attention TFLOP/s and % of the int8 MFMA peak at
 H=32, D=128, S=16896; ms per call).
 
     python bench.py [--gpus 1] [--steps 20] [--warmup 10] [--config c4] [--no-cpu]
 
 A step is one attention call over the whole workload (all heads, all query rows) with its inputs resident in
-HBM. The default workload is BASELINE config 4: B=1, H=32, D=128, S=16896 (512 text + 16384 image rows), Q/K bf16
+HBM. The default workload is benchmark config 4: B=1, H=32, D=128, S=16896 (512 text + 16384 image rows), Q/K bf16
 ~N(0,1) with 4 of 128 channels per head x20, rotated and quantised to int8 by the fused pre-pass (timed
 separately, reported under "prepass"), V bf16 ~N(0,1), int8 QK^T + bf16 P V. The attention output's consumer,
 rot_q8 (256-block Hadamard + per-row int8 of O), is timed on the call's own output and reported under "rot_q8";
@@ -188,7 +188,7 @@ def main():
         "ms_per_step": round(ms, 4), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
         "dtype": "int8 QK^T (int32 acc) + bf16 PV (fp32 acc)" if path == "int8" else "bf16 (fp32 acc)",
         "data": "synthetic (seeded N(0,1); config-4 outlier recipe)",
-        "config": {"workload": f"BASELINE {args.config}: B=1 H={H} D={D} Sq={S} Sk_valid={L}, non-causal, "
+        "config": {"workload": f"{args.config}: B=1 H={H} D={D} Sq={S} Sk_valid={L}, non-causal, "
                                f"{'Hadamard-rotated int8 Q/K + bf16 V' if path == 'int8' else 'bf16 Q/K/V'}",
                    "global_batch": 1, "seq_len": S, "parallelism": "single GPU"},
         "pct_of_peak": round(100 * value * 1e12 / peak, 2),

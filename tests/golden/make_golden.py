@@ -4,7 +4,7 @@
 
 The reference ships no golden vectors for this path (its kernels are Metal
 code that cannot run here), so these fixtures freeze the oracle's output on
-seeded inputs of the BASELINE config-4 recipe (N(0,1) with 4 of 128 channels
+seeded inputs of the benchmark config-4 recipe (N(0,1) with 4 of 128 channels
 per head x20, bf16) at a small size. tests/test_oracle.py checks that the
 oracle still reproduces them; the GPU tests compare the HIP kernels with them.
 """

@@ -5,7 +5,7 @@
 * Outputs: the reference's own cases (tests/test_attention.py: check :23-56 with half inputs, check_q8 :60-114
   with int8 scores, temp/ramp stresses, GQA, causal, D=64) with its tolerance 5e-3 max-abs against float64;
   the north-star tolerance (2e-2 max-abs, 1e-3 mean-abs against fp32/float64) for the bf16 paths and the
-  BASELINE configs.
+  benchmark configs.
 """
 
 import numpy as np
@@ -208,7 +208,7 @@ def test_causal_offset(gpu):
     assert np.abs(got[:Lq] - ref).max() < 5e-3
 
 
-# -- BASELINE configs ------------------------------------------------------------------------------------------------
+# -- benchmark configs ------------------------------------------------------------------------------------------------
 
 def test_config1_plumbing(gpu):
     """Config 1: B=1, H=4, S=256, D=128, fp32 N(0,1), scale 1/sqrt(128), no mask, vs the numpy reference of the
@@ -318,7 +318,7 @@ def test_config4_int8_rotated_full_size(gpu):
     assert err.max() < NS_MAX and err.mean() < NS_MEAN, (err.max(), err.mean())
 
 
-# -- other callers' variants -----------------------------------------------------------------------------
+# -- other callers' variants -------------------------------------------------------------------------------------------
 
 @pytest.mark.parametrize("dtype,H,KVH,causal", [("f16", 4, 2, False), ("f16", 4, 4, True), ("bf16", 3, 3, False)])
 def test_head_dim_96(gpu, dtype, H, KVH, causal):

@@ -1,6 +1,6 @@
 """The fused pre-pass kernel (ops.qk_norm_rope) against the float32 oracle: int8 codes and scales bit-exact,
 16-bit outputs exact up to the output rounding. Mirrors the reference's tests/test_ops.py::test_qk (:80-111) and
-tests/test_qk_rotation.py, plus the BASELINE config-4 recipe at full size on sampled rows."""
+tests/test_qk_rotation.py, plus the benchmark config-4 recipe at full size on sampled rows."""
 
 import os
 
@@ -176,7 +176,7 @@ def test_zero_rows_scale_one(gpu):
 
 
 def test_config4_full_size_sampled_rows(gpu):
-    """BASELINE config 4 at full size (H=32, S=16896): the kernel runs over all rows; the oracle checks a seeded
+    """Benchmark config 4 at full size (H=32, S=16896): the kernel runs over all rows; the oracle checks a seeded
     sample of 512 rows bit for bit (the pre-pass is row-independent), and every row satisfies the int8
     invariants (max |code| = 127 for non-zero rows, dequantised rows within half a step of the rotated input's
     norm-preserving image)."""
