@@ -318,6 +318,43 @@ def test_config4_int8_rotated_full_size(gpu):
     assert err.max() < NS_MAX and err.mean() < NS_MEAN, (err.max(), err.mean())
 
 
+def test_config5_int8_rotated_full_size(gpu):
+    """Config 5 at full size (H=32, D=128, S=66048, the config-4 recipe): pre-pass and int8 attention over all rows
+    and keys; a seeded sample of query rows against float64 attention of the dequantised int8 inputs, head by
+    head."""
+    rng = np.random.default_rng(5)
+    H, D, S = 32, 128, 66048
+    X = gpu.empty((S, 3 * H * D), "bf16")
+    out_ch = [rng.choice(D, 4, replace=False) for _ in range(2 * H)]
+    for r0 in range(0, S, 4096):  # generated in row chunks to bound host memory
+        n = min(4096, S - r0)
+        x = rng.standard_normal((n, 3, H, D), dtype=np.float32)
+        for part in (0, 1):
+            for h in range(H):
+                x[:, part, h, out_ch[part * H + h]] *= 20
+        X.write(to_bf16(x.reshape(n, -1)), offset_elems=r0 * 3 * H * D)
+    Q, K = gpu.empty((H, S, D), "i8"), gpu.empty((H, S, D), "i8")
+    V = gpu.empty((H, S, D), "bf16")
+    qs, ks = gpu.empty((H, S), "f32"), gpu.empty((H, S), "f32")
+    print("[config5] pre-pass + attention", flush=True)
+    ops.qk_norm_rope(gpu, X, None, None, None, None, Q, K, V, M=S, Hq=H, Hk=H, Hv=H, hd=D, out_rows=S, rot=0,
+                     eps=1e-6, norm=False, q_scale=qs, k_scale=ks, qk_rot=True)
+    O = gpu.empty((S, H * D), "bf16")
+    ops.attention(gpu, Q, K, V, O, Lq=S, L=S, H=H, KVH=H, D=D, q_rows=S, k_rows=S, scale=D ** -0.5, q_scale=qs,
+                  k_scale=ks)
+    gpu.wait()
+    qi, ki, qsh, ksh, vb = Q.numpy(), K.numpy(), qs.numpy(), ks.numpy(), V.numpy()
+    got = from_bf16(O.numpy()).astype(np.float64)
+    rows = np.sort(rng.choice(S, 48, replace=False))
+    ref = np.zeros((len(rows), H * D))
+    for h in range(H):
+        qd = (qi[h, rows] * qsh[h, rows, None].astype(np.float64))[None]
+        kd = (ki[h] * ksh[h, :, None].astype(np.float64))[None]
+        ref[:, h * D:(h + 1) * D] = oa.ref_attention(qd, kd, from_bf16(vb[h])[None], D ** -0.5)
+    err = np.abs(got[rows] - ref)
+    assert err.max() < NS_MAX and err.mean() < NS_MEAN, (err.max(), err.mean())
+
+
 # -- other callers' variants -------------------------------------------------------------------------------------------
 
 @pytest.mark.parametrize("dtype,H,KVH,causal", [("f16", 4, 2, False), ("f16", 4, 4, True), ("bf16", 3, 3, False)])
