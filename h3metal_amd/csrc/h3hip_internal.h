@@ -85,12 +85,14 @@ bool make_rot_q8(const Macros &m, Pipeline *pl, std::string *err);  // module "o
 bool make_gemm(const std::string &fn, const Macros &m, Pipeline *pl, std::string *err);
 
 // Wave64 lane exchanges inside a 32-lane half wave, shared by the row kernels: the value of lane (lane ^ S).
-// DPP for S = 1, 2 (quad_perm), ds_swizzle's xor mode (no LDS memory access) for S = 4, 8, 16.
+// DPP for S = 1, 2 (quad_perm) and 8 (row_ror:8, a 16-lane rotation by 8), ds_swizzle's xor mode (no LDS
+// memory access) for S = 4, 16.
 template <int S>
 __device__ __forceinline__ float xshfl(float v) {
   const int x = __builtin_bit_cast(int, v);
-  if constexpr (S == 1) return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, x, 0xB1, 0xF, 0xF, false));
-  else if constexpr (S == 2) return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, x, 0x4E, 0xF, 0xF, false));
+  if constexpr (S == 1) return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, x, 0xB1, 0xF, 0xF, true));
+  else if constexpr (S == 2) return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, x, 0x4E, 0xF, 0xF, true));
+  else if constexpr (S == 8) return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, x, 0x128, 0xF, 0xF, true));
   else return __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(x, 0x1F | (S << 10)));
 }
 
