@@ -96,6 +96,40 @@ __device__ __forceinline__ float xshfl(float v) {
   else return __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(x, 0x1F | (S << 10)));
 }
 
+// One cross-lane stage of a Walsh-Hadamard transform over lane bit LS, on N values per lane: every lane
+// computes own + c * partner with c = +1 on the lower lane of a pair and -1 on the upper one. The lower lane gets
+// a + b, the upper b - a = -(a - b); partners share every other lane bit, so after stages over a set of lane bits
+// a lane holds its true values times (-1)^(number of those bits set in the lane id), which the caller folds into
+// its final scale (an exact sign change). The product with c is exact and the one rounding is that of the sum,
+// the same as for a + b or a - b (rounding is sign-symmetric). For LS = 1, 2, 8 the shuffled value is the
+// multiplicand of an fmac that reads it straight through DPP (written as assembly, since the compiler keeps a
+// separate DPP move); the leading s_nop gives each DPP read the two wait states it needs after the VALU write
+// of its source, and within a stage each value was written N instructions earlier.
+template <int LS, int N>
+__device__ __forceinline__ void hadamard_lane_stage(float (&v)[N], float c) {
+  if constexpr (LS == 1 || LS == 2 || LS == 8) {
+    asm volatile("s_nop 1");
+#pragma unroll
+    for (int i = 0; i < N; i++) {
+      if constexpr (LS == 1)
+        asm volatile("v_fmac_f32_dpp %0, %0, %1 quad_perm:[1,0,3,2] row_mask:0xf bank_mask:0xf bound_ctrl:1"
+                     : "+v"(v[i])
+                     : "v"(c));
+      else if constexpr (LS == 2)
+        asm volatile("v_fmac_f32_dpp %0, %0, %1 quad_perm:[2,3,0,1] row_mask:0xf bank_mask:0xf bound_ctrl:1"
+                     : "+v"(v[i])
+                     : "v"(c));
+      else
+        asm volatile("v_fmac_f32_dpp %0, %0, %1 row_ror:8 row_mask:0xf bank_mask:0xf bound_ctrl:1"
+                     : "+v"(v[i])
+                     : "v"(c));
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < N; i++) v[i] = __builtin_fmaf(xshfl<LS>(v[i]), c, v[i]);
+  }
+}
+
 // Helpers for macro parsing in the factories.
 bool macro_int(const Macros &m, const char *key, int def, int *out, std::string *err);
 std::string macro_str(const Macros &m, const char *key, const char *def);

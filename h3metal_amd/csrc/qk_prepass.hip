@@ -162,39 +162,11 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kernel(const char *__restric
           }
         }
         // across lanes: channel c pairs with c ^ (ls * PER), stages in increasing bit order; the lower channel
-        // becomes a + b, the upper one a - b (a the lower channel's value). Each lane computes own + c * partner
-        // with c = +1 (lower) or -1 (upper): the lower lane gets a + b, the upper one b - a = -(a - b), so after
-        // the stages a lane holds its true value times (-1)^(number of upper positions) = (-1)^popcount(l32)
-        // (partners share every other lane bit, so they carry the same sign). The product with c is exact and
-        // the one rounding is that of the sum, the same as for a + b and a - b (rounding is sign-symmetric).
-        // In this form the shuffled value is the multiplicand of an fmac, which reads it straight through DPP
-        // (quad_perm for lane bits 1 and 2, row_ror:8 for bit 8; written as assembly, since the compiler keeps
-        // a separate DPP move). The leading s_nop gives the DPP read of v the two wait states it needs after the
-        // VALU instruction that last wrote it; within a stage each v[i] was written PER instructions earlier.
+        // becomes a + b, the upper one a - b (a the lower channel's value); each lane ends with its values
+        // times (-1)^popcount(l32) (hadamard_lane_stage)
         auto stage = [&](auto ls_const) {
           constexpr int LS = decltype(ls_const)::value;
-          const float c = (l32 & LS) ? -1.0f : 1.0f;
-          if constexpr (LS == 1 || LS == 2 || LS == 8) {
-            asm volatile("s_nop 1");
-#pragma unroll
-            for (int i = 0; i < PER; i++) {
-              if constexpr (LS == 1)
-                asm volatile("v_fmac_f32_dpp %0, %0, %1 quad_perm:[1,0,3,2] row_mask:0xf bank_mask:0xf bound_ctrl:1"
-                             : "+v"(v[i])
-                             : "v"(c));
-              else if constexpr (LS == 2)
-                asm volatile("v_fmac_f32_dpp %0, %0, %1 quad_perm:[2,3,0,1] row_mask:0xf bank_mask:0xf bound_ctrl:1"
-                             : "+v"(v[i])
-                             : "v"(c));
-              else
-                asm volatile("v_fmac_f32_dpp %0, %0, %1 row_ror:8 row_mask:0xf bank_mask:0xf bound_ctrl:1"
-                             : "+v"(v[i])
-                             : "v"(c));
-            }
-          } else {
-#pragma unroll
-            for (int i = 0; i < PER; i++) v[i] = fmaf(xshfl<LS>(v[i]), c, v[i]);
-          }
+          hadamard_lane_stage<LS>(v, (l32 & LS) ? -1.0f : 1.0f);
         };
         stage(std::integral_constant<int, 1>{});
         stage(std::integral_constant<int, 2>{});

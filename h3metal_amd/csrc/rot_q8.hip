@@ -90,21 +90,21 @@ __global__ __launch_bounds__(256) void rot_q8_kernel(const char *__restrict__ in
           v[b][i] = a + c;
           v[b][i + s] = a - c;
         }
-    // lower column keeps v + o, upper o - v: fma(+-1, v, o), an exact product and one rounding
+    // across lanes (column bits 3-7): the lower column becomes a + b, the upper a - b; each lane ends with its
+    // values times (-1)^popcount(l32), folded into the final 1/16 (hadamard_lane_stage)
     auto stage = [&](auto ls_const) {
       constexpr int LS = decltype(ls_const)::value;
-      const float sg = (l32 & LS) ? -1.0f : 1.0f;
-#pragma unroll
-      for (int i = 0; i < 8; i++) v[b][i] = fmaf(sg, v[b][i], xshfl<LS>(v[b][i]));
+      hadamard_lane_stage<LS>(v[b], (l32 & LS) ? -1.0f : 1.0f);
     };
     stage(std::integral_constant<int, 1>{});
     stage(std::integral_constant<int, 2>{});
     stage(std::integral_constant<int, 4>{});
     stage(std::integral_constant<int, 8>{});
     stage(std::integral_constant<int, 16>{});
+    const float sc = (__builtin_popcount(l32) & 1) ? -0.0625f : 0.0625f;
 #pragma unroll
     for (int i = 0; i < 8; i++) {
-      v[b][i] *= 0.0625f;
+      v[b][i] *= sc;
       amax = fmaxf(amax, fabsf(v[b][i]));
     }
   }
