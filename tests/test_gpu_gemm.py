@@ -38,7 +38,8 @@ def run(gpu, a, sa, q, sw, b, M, out_dtype="f32", tile=(64, 128, 4)):
 
 
 @pytest.mark.parametrize("M,N,K,bias", [(200, 256, 512, False), (300, 640, 384, True), (64, 1024, 128, True),
-                                        (1, 256, 256, False), (513, 512, 1280, False)])
+                                        (1, 256, 256, False), (513, 512, 1280, False),
+                                        (70, 256, 64, True), (130, 512, 192, False)])
 def test_f32_outputs_bit_exact(gpu, M, N, K, bias):
     rng = np.random.default_rng(M + N + K)
     a, sa, q, sw, b = make(rng, M, N, K, bias=bias)
@@ -183,7 +184,7 @@ def test_refusals(gpu):
         ops.gemm(gpu, A, wt, out, 64, sa=SA, tile=(32, 512, 8))
     with pytest.raises(NotImplementedError):
         ops.gemm(gpu, A, ops.QWeight("q4", wt.w, wt.sw, 256, 256), out, 64, sa=SA)
-    with pytest.raises(GpuError):  # K must be a multiple of 128
+    with pytest.raises(GpuError):  # K must be a multiple of 64
         ops.gemm(gpu, A, ops.QWeight("q8", wt.w, wt.sw, 256, 200, ws=256), out, 64, sa=SA, a_stride=256)
     with pytest.raises(GpuError):  # the output does not hold M padded rows
         ops.gemm(gpu, A, wt, gpu.empty((32, 256), "f16"), 64, sa=SA)
