@@ -604,42 +604,6 @@ __global__ __launch_bounds__(256) void attention_merge(const float *__restrict__
 
 int esize(int t) { return t == T_I8 ? 1 : t == T_F32 ? 4 : 2; }
 
-// CUs of the current device (the tail split sizes itself to them), cached per device.
-int cu_count() {
-  static int cache[64] = {};
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
-  if (!cache[dev]) {
-    int n = 0;
-    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
-    cache[dev] = n;
-  }
-  return cache[dev];
-}
-
-// Partial-state workspace of the tail split, per stream (work on one stream is ordered, so one buffer per
-// stream is never used by two launches at once); grown on demand and kept until the process ends.
-float *split_workspace(hipStream_t stream, size_t bytes, std::string *err) {
-  static std::mutex mu;
-  static std::map<hipStream_t, std::pair<void *, size_t>> bufs;
-  std::lock_guard<std::mutex> lock(mu);
-  auto &e = bufs[stream];
-  if (e.second < bytes) {
-    if (e.first) {
-      hipStreamSynchronize(stream);  // the old buffer may still be read by queued work
-      hipFree(e.first);
-      e = {nullptr, 0};
-    }
-    void *ptr = nullptr;
-    if (hipMalloc(&ptr, bytes) != hipSuccess) {
-      *err = "attention: cannot allocate the " + std::to_string(bytes) + "-byte split workspace";
-      return nullptr;
-    }
-    e = {ptr, bytes};
-  }
-  return (float *)e.first;
-}
-
 // Host side: validation (every access the kernel makes must fall inside the
 // bound buffers) and launch.
 template <int D, int QKT, int VT, int OT, bool CAUSAL, bool DUMP>
@@ -729,7 +693,7 @@ int launch_attention(const Pipeline &pl, hipStream_t stream, const Arg *args, in
       sp.cb = cb;
       sp.nfull = (int)ntiles - R;
       const size_t bytes = (size_t)R * sp.s * C::BQ * (D + 4) * sizeof(float);
-      sp.ws = split_workspace(stream, bytes, err);
+      sp.ws = (float *)split_workspace(stream, bytes, "attention", err);
       if (!sp.ws) return -1;
     }
   }

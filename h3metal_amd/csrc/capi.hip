@@ -12,6 +12,7 @@
 
 #include <algorithm>
 #include <cstring>
+#include <map>
 #include <memory>
 #include <mutex>
 #include <vector>
@@ -79,6 +80,44 @@ bool macro_int(const Macros &m, const char *key, int def, int *out, std::string 
 std::string macro_str(const Macros &m, const char *key, const char *def) {
   auto it = m.find(key);
   return it == m.end() ? std::string(def) : it->second;
+}
+
+
+// CUs of the current device (the tail splits size themselves to them), cached per device.
+int cu_count() {
+  static int cache[64] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
+  if (!cache[dev]) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
+    cache[dev] = n;
+  }
+  return cache[dev];
+}
+
+// Workspace of the tail splits (attention's partial states, the GEMM's partial products), per stream: work on
+// one stream is ordered, so one buffer per stream is never used by two launches at once; grown on demand and
+// kept until the process ends.
+void *split_workspace(hipStream_t stream, size_t bytes, const char *who, std::string *err) {
+  static std::mutex mu;
+  static std::map<hipStream_t, std::pair<void *, size_t>> bufs;
+  std::lock_guard<std::mutex> lock(mu);
+  auto &e = bufs[stream];
+  if (e.second < bytes) {
+    if (e.first) {
+      hipStreamSynchronize(stream);  // the old buffer may still be read by queued work
+      hipFree(e.first);
+      e = {nullptr, 0};
+    }
+    void *ptr = nullptr;
+    if (hipMalloc(&ptr, bytes) != hipSuccess) {
+      *err = std::string(who) + ": cannot allocate the " + std::to_string(bytes) + "-byte split workspace";
+      return nullptr;
+    }
+    e = {ptr, bytes};
+  }
+  return e.first;
 }
 
 }  // namespace h3

@@ -130,6 +130,11 @@ __device__ __forceinline__ void hadamard_lane_stage(float (&v)[N], float c) {
   }
 }
 
+// Compute units of the current device (0 if unknown), and the per-stream scratch buffer of the tail splits
+// (at least `bytes`, grown on demand, kept until the process ends; NULL with a message on failure).
+int cu_count();
+void *split_workspace(hipStream_t stream, size_t bytes, const char *who, std::string *err);
+
 // Helpers for macro parsing in the factories.
 bool macro_int(const Macros &m, const char *key, int def, int *out, std::string *err);
 std::string macro_str(const Macros &m, const char *key, const char *def);
