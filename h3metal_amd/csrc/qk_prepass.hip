@@ -103,6 +103,12 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kernel(const char *__restric
     return ((size_t)sq * heads + h) * p.out_rows + r;
   };
   float keep = 1.0f;  // lane l32 < nr: the scale of row m0 + l32
+  // QKROT's fixed signs: channel c = l32 * PER + i is negated when popcount(c * 0x2545F491) is odd (its sign
+  // bit, flipped by an xor; computed once per lane)
+  unsigned sbit[PER];
+#pragma unroll
+  for (int i = 0; i < PER; i++)
+    sbit[i] = (__builtin_popcount((unsigned)(l32 * PER + i) * 0x2545F491u) & 1u) ? 0x80000000u : 0u;
 
 #pragma unroll
   for (int rr = 0; rr < RPW; rr++) {
@@ -146,10 +152,7 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kernel(const char *__restric
       }
       if constexpr (QKROT) {
 #pragma unroll
-        for (int i = 0; i < PER; i++) {
-          const unsigned c = (unsigned)(l32 * PER + i);
-          if (__builtin_popcount(c * 0x2545F491u) & 1u) v[i] = -v[i];
-        }
+        for (int i = 0; i < PER; i++) v[i] = __builtin_bit_cast(float, __builtin_bit_cast(unsigned, v[i]) ^ sbit[i]);
 #pragma unroll
         for (int s = 1; s < PER; s <<= 1) {
 #pragma unroll
