@@ -192,15 +192,16 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kernel(const char *__restric
         amax = fmaxf(amax, xshfl<2>(amax));
         amax = fmaxf(amax, xshfl<1>(amax));
         const float scale = amax > 0.0f ? amax / 127.0f : 1.0f;
-        const float rs = 1.0f / scale;
+        const float rs = __builtin_amdgcn_rcpf(scale);  // 1 ulp
         typedef typename VecOf<PER, signed char>::type CV;
         CV codes;
 #pragma unroll
         for (int i = 0; i < PER; i++) codes[i] = (signed char)(int)rintf(v[i] * rs);
-        // v * fl(1/scale) is within 2 ulp of the correctly rounded quotient v / scale, so its nearest integer is
-        // the quotient's unless it lies within a few ulp of a half-integer (ulp <= 2^-17 below 128): then the
-        // lanes concerned divide (rare, and exact).
-        bool near_half = false;
+        // |v / scale| <= 127.5 and rs is within 1 ulp of 1/scale, so v * rs is within 2^-16 + 2^-18 < 2^-15 of
+        // the exact quotient: its nearest integer is the quotient's unless it lies within 2^-15 of a
+        // half-integer, and then the lanes concerned divide (rare, and exact). A scale whose reciprocal is not
+        // a normal float (amax below ~2^-119) divides on every lane.
+        bool near_half = !(rs < 0x1p126f);
 #pragma unroll
         for (int i = 0; i < PER; i++) {
           const float y = v[i] * rs;

@@ -175,6 +175,23 @@ def test_zero_rows_scale_one(gpu):
     assert (got["Q"] == 0).all() and (got["qs"][:, :5] == 1).all() and (got["ks"][:, :5] == 1).all()
 
 
+@pytest.mark.parametrize("mag", [1e-40, 1e-38, 1e-36, 1e-30, 3e-20, 1e4])
+def test_tiny_and_large_rows_bit_exact(gpu, mag):
+    """Rows whose scale is subnormal or whose reciprocal is out of range (amax below ~2^-119) take the exact
+    division for every value; ordinary magnitudes at both ends stay bit-exact too (f32 input, so the tiny
+    values are representable)."""
+    rng = np.random.default_rng(int(-np.log10(mag)) + 50)
+    M, H = 9, 2
+    x = (rng.standard_normal((M, 3 * H * 128)) * mag).astype(np.float32)
+    got = run_prepass(gpu, x, "f32", M=M, Hq=H, Hk=H, Hv=H, hd=128, out_rows=16)
+    want = op.qk_norm_rope(x, Hq=H, Hk=H, Hv=H, hd=128, out_rows=16, rot=0, eps=1e-6, norm=False, q8=True,
+                           qk_rot=True)
+    for n in ("Q", "K"):
+        assert np.array_equal(got[n], want[n]), (n, mag, np.argwhere(got[n] != want[n])[:5])
+    for n in ("qs", "ks"):
+        assert np.array_equal(got[n].view(np.uint32), want[n].view(np.uint32)), (n, mag)
+
+
 def test_config4_full_size_sampled_rows(gpu):
     """Benchmark config 4 at full size (H=32, S=16896): the kernel runs over all rows; the oracle checks a seeded
     sample of 512 rows bit for bit (the pre-pass is row-independent), and every row satisfies the int8
