@@ -224,10 +224,14 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kernel(const char *__restric
     } else {
       using OE = typename Elem<V_T>::type;
       typedef typename VecOf<PER, OE>::type OV;
-      OV out;
+      if constexpr (V_T == IN_T) {
+        *(OV *)(Vo + (hrow * HDIM + l32 * PER) * sizeof(OE)) = xin[rr];  // same type: a plain copy
+      } else {
+        OV out;
 #pragma unroll
-      for (int i = 0; i < PER; i++) out[i] = (OE)v[i];
-      *(OV *)(Vo + (hrow * HDIM + l32 * PER) * sizeof(OE)) = out;
+        for (int i = 0; i < PER; i++) out[i] = (OE)v[i];
+        *(OV *)(Vo + (hrow * HDIM + l32 * PER) * sizeof(OE)) = out;
+      }
     }
   }
   if constexpr (QK_T == T_I8) {
