@@ -25,12 +25,36 @@
 
 #include <algorithm>
 #include <cstring>
+#include <type_traits>
 
 namespace h3 {
 namespace {
 
 typedef int i32x4 __attribute__((ext_vector_type(4)));
 typedef int i32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+
+// operand types of a kernel: int8 (q8), half (f16, and h8 after its weights are widened), bfloat (bf16)
+enum { A_I8 = 0, A_F16 = 1, A_BF16 = 2 };
+// epilogue scaling: sa[m] * sw[n] (q8), sw[n] (h8), none (f16, bf16)
+enum { S_ROW_COL = 0, S_COL = 1, S_NONE = 2 };
+
+template <int AT>
+using AccOf = typename std::conditional<AT == A_I8, i32x16, f32x16>::type;
+
+// one 32 x 32 product over a 32-byte K slice per lane half (32 int8 or 16 16-bit values of K)
+template <int AT>
+__device__ __forceinline__ AccOf<AT> mma(i32x4 a, i32x4 b, AccOf<AT> c) {
+  if constexpr (AT == A_I8) return __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b, c, 0, 0, 0);
+  else if constexpr (AT == A_F16)
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c, 0,
+                                                  0, 0);
+  else
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c,
+                                                   0, 0, 0);
+}
 
 enum { T_BF16 = 1, T_F16 = 2, T_F32 = 3 };
 
@@ -63,9 +87,9 @@ __device__ __forceinline__ void store_out(char *p, float v) {
   else *(_Float16 *)p = (_Float16)v;
 }
 
-template <int OT, int EPI, bool HAS_BIAS>
-__global__ __launch_bounds__(NWG * 64) __attribute__((amdgpu_waves_per_eu(2))) void gemm_q8_kernel(const signed char *__restrict__ A,
-                                                           const signed char *__restrict__ W,
+template <int OT, int EPI, bool HAS_BIAS, int AT, int SM>
+__global__ __launch_bounds__(NWG * 64) __attribute__((amdgpu_waves_per_eu(2))) void gemm_kernel(const char *__restrict__ A,
+                                                           const char *__restrict__ W,
                                                            const float *__restrict__ sw, const float *__restrict__ sa,
                                                            char *__restrict__ out, const float *__restrict__ bias,
                                                            const unsigned char *__restrict__ rtype,
@@ -77,6 +101,9 @@ __global__ __launch_bounds__(NWG * 64) __attribute__((amdgpu_waves_per_eu(2))) v
   const int wm = w / WGN, wn = w % WGN;
   // accumulators hold C^T for the plain outputs (staged through LDS), C for the residual form
   constexpr bool TR = EPI == 0;
+  // byte strides and K in bytes (the parameter block counts elements)
+  constexpr int ES = AT == A_I8 ? 1 : 2;
+  const int astr = p.a_stride * ES, wstr = p.w_stride * ES;
 
   // tile order: XCD-contiguous ranges (workgroup b runs on XCD b % 8), then bands of SW row tiles
   const int nb = gridDim.x, b = blockIdx.x;
@@ -89,13 +116,13 @@ __global__ __launch_bounds__(NWG * 64) __attribute__((amdgpu_waves_per_eu(2))) v
 
   // staging: 4 A pieces and 4 W pieces of 16 bytes per thread and step; rows >= M (N) read as zero
   // (the record counts are wave-uniform; readfirstlane keeps the descriptors in scalar registers)
-  const int reca = __builtin_amdgcn_readfirstlane(max(0, min(TM, p.M - m0)) * p.a_stride);
-  const int recw = __builtin_amdgcn_readfirstlane(max(0, min(TN, p.N - n0)) * p.w_stride);
+  const int reca = __builtin_amdgcn_readfirstlane(max(0, min(TM, p.M - m0)) * astr);
+  const int recw = __builtin_amdgcn_readfirstlane(max(0, min(TN, p.N - n0)) * wstr);
   const __amdgpu_buffer_rsrc_t ra =
-      __builtin_amdgcn_make_buffer_rsrc((void *)(A + (size_t)m0 * p.a_stride), (short)0, reca, 0x00020000);
+      __builtin_amdgcn_make_buffer_rsrc((void *)(A + (size_t)m0 * astr), (short)0, reca, 0x00020000);
   const __amdgpu_buffer_rsrc_t rw =
-      __builtin_amdgcn_make_buffer_rsrc((void *)(W + (size_t)n0 * p.w_stride), (short)0, recw, 0x00020000);
-  const int nk = p.K / KS;
+      __builtin_amdgcn_make_buffer_rsrc((void *)(W + (size_t)n0 * wstr), (short)0, recw, 0x00020000);
+  const int nk = p.K * ES / KS;
   // staging: a stage is 512 rows of 64 bytes (A rows 0-255, then W rows); one wave load fills 16 rows, lane l
   // the slot l % 4 of row l / 4, with the source piece that the reader's swizzle expects there. Wave w loads
   // rows 32 w .. 32 w + 31 of A and of W. Steps past the last read zero (offset 2^31, beyond the records).
@@ -103,9 +130,9 @@ __global__ __launch_bounds__(NWG * 64) __attribute__((amdgpu_waves_per_eu(2))) v
   const int lrow = lane >> 2, lpiece = (lane & 3) ^ ((lane >> 4) & 3);
   int offa[NQA], offw[NQW];
 #pragma unroll
-  for (int q = 0; q < NQA; q++) offa[q] = (16 * (NQA * w + q) + lrow) * p.a_stride + lpiece * 16;
+  for (int q = 0; q < NQA; q++) offa[q] = (16 * (NQA * w + q) + lrow) * astr + lpiece * 16;
 #pragma unroll
-  for (int q = 0; q < NQW; q++) offw[q] = (16 * (NQW * w + q) + lrow) * p.w_stride + lpiece * 16;
+  for (int q = 0; q < NQW; q++) offw[q] = (16 * (NQW * w + q) + lrow) * wstr + lpiece * 16;
   auto dma = [&](int kt) __attribute__((always_inline)) {
     const unsigned st = lds0 + ((unsigned)kt % NST) * STAGE;
     const bool ok = kt < nk;
@@ -117,7 +144,7 @@ __global__ __launch_bounds__(NWG * 64) __attribute__((amdgpu_waves_per_eu(2))) v
       dma16(st + (TM + 16 * (NQW * w + q)) * KS, ok ? offw[q] + kt * KS : (int)0x80000000u, rw);
   };
 
-  i32x16 acc[MI][NJ];
+  AccOf<AT> acc[MI][NJ];
 #pragma unroll
   for (int i = 0; i < MI; i++)
 #pragma unroll
@@ -153,8 +180,7 @@ __global__ __launch_bounds__(NWG * 64) __attribute__((amdgpu_waves_per_eu(2))) v
       for (int i = 0; i < MI; i++)
 #pragma unroll
         for (int j = 0; j < NJ; j++)
-          acc[i][j] = TR ? __builtin_amdgcn_mfma_i32_32x32x32_i8(cur.w[c][j], cur.a[c][i], acc[i][j], 0, 0, 0)
-                         : __builtin_amdgcn_mfma_i32_32x32x32_i8(cur.a[c][i], cur.w[c][j], acc[i][j], 0, 0, 0);
+          acc[i][j] = TR ? mma<AT>(cur.w[c][j], cur.a[c][i], acc[i][j]) : mma<AT>(cur.a[c][i], cur.w[c][j], acc[i][j]);
     constexpr int NR = 2 * (MI + NJ), NF = 2 * MI * NJ;  // LDS reads and MFMAs of a step
 #pragma unroll
     for (int g = 0; g < NR; g++) {
@@ -191,7 +217,7 @@ __global__ __launch_bounds__(NWG * 64) __attribute__((amdgpu_waves_per_eu(2))) v
 #pragma unroll
       for (int e = 0; e < 16; e++) {
         const int m = min(row_of(i, e), p.M - 1);
-        sam[e] = sa[m];
+        if constexpr (SM == S_ROW_COL) sam[e] = sa[m];
         // row types past the gate table's rows clamp to its last
         goff[e] = min((int)rtype[m], ntypes - 1) * p.g_stride;
       }
@@ -200,7 +226,7 @@ __global__ __launch_bounds__(NWG * 64) __attribute__((amdgpu_waves_per_eu(2))) v
         const int n = n0 + WTN * wn + 32 * j + l32;
         const bool nok = n < p.N;
         const int nc = min(n, p.N - 1);
-        const float swn = sw[nc];
+        const float swn = SM != S_NONE ? sw[nc] : 1.0f;
         const float bn = HAS_BIAS ? bias[nc] : 0.0f;
         float xv[16], gv[16];
 #pragma unroll
@@ -211,7 +237,9 @@ __global__ __launch_bounds__(NWG * 64) __attribute__((amdgpu_waves_per_eu(2))) v
 #pragma unroll
         for (int e = 0; e < 16; e++) {
           const int m = row_of(i, e);
-          float v = (float)acc[i][j][e] * sam[e] * swn;
+          float v = (float)acc[i][j][e];
+          if constexpr (SM == S_ROW_COL) v = v * sam[e] * swn;
+          else if constexpr (SM == S_COL) v = v * swn;
           if constexpr (HAS_BIAS) v += bn;
           if (nok && m < p.M) ((float *)out)[(size_t)m * p.c_stride + n] = xv[e] + gv[e] * v;
         }
@@ -226,9 +254,11 @@ __global__ __launch_bounds__(NWG * 64) __attribute__((amdgpu_waves_per_eu(2))) v
   constexpr int OSZ = OT == T_F32 ? 4 : 2;
   float sam[MI];
 #pragma unroll
-  for (int i = 0; i < MI; i++) sam[i] = sa[min(m0 + WTM * wm + 32 * i + l32, p.M - 1)];
+  for (int i = 0; i < MI; i++) sam[i] = SM == S_ROW_COL ? sa[min(m0 + WTM * wm + 32 * i + l32, p.M - 1)] : 1.0f;
   auto value = [&](int i, int j, int e, float swn, float bn) __attribute__((always_inline)) {
-    float v = (float)acc[i][j][e] * sam[i] * swn;
+    float v = (float)acc[i][j][e];
+    if constexpr (SM == S_ROW_COL) v = v * sam[i] * swn;
+    else if constexpr (SM == S_COL) v = v * swn;
     if constexpr (HAS_BIAS) v += bn;
     return v;
   };
@@ -255,7 +285,8 @@ __global__ __launch_bounds__(NWG * 64) __attribute__((amdgpu_waves_per_eu(2))) v
 #pragma unroll
       for (int q = 0; q < 4; q++) {
         const int nl = WTN * wn + 32 * j + 8 * q + 4 * hl, n = n0 + nl;
-        const float4 s4 = ld4(sw, min(n, vec ? p.N - 4 : n));
+        float4 s4 = {1, 1, 1, 1};
+        if constexpr (SM != S_NONE) s4 = ld4(sw, min(n, vec ? p.N - 4 : n));
         float4 b4 = {0, 0, 0, 0};
         if constexpr (HAS_BIAS) b4 = ld4(bias, min(n, vec ? p.N - 4 : n));
         const float sv[4] = {s4.x, s4.y, s4.z, s4.w}, bv[4] = {b4.x, b4.y, b4.z, b4.w};
@@ -302,7 +333,8 @@ __global__ __launch_bounds__(NWG * 64) __attribute__((amdgpu_waves_per_eu(2))) v
 #pragma unroll
           for (int q = 0; q < 4; q++) {
             const int nl = WTN * wn + 32 * j + 8 * q + 4 * hl, n = n0 + nl;
-            const float4 s4 = ld4(sw, min(n, vec ? p.N - 4 : n));
+            float4 s4 = {1, 1, 1, 1};
+        if constexpr (SM != S_NONE) s4 = ld4(sw, min(n, vec ? p.N - 4 : n));
             float4 b4 = {0, 0, 0, 0};
             if constexpr (HAS_BIAS) b4 = ld4(bias, min(n, vec ? p.N - 4 : n));
             const float sv[4] = {s4.x, s4.y, s4.z, s4.w}, bv[4] = {b4.x, b4.y, b4.z, b4.w};
@@ -337,10 +369,29 @@ __global__ __launch_bounds__(NWG * 64) __attribute__((amdgpu_waves_per_eu(2))) v
   }
 }
 
-template <int OT, int EPI, bool HAS_BIAS>
+// h8 weights: the int8 codes widened to half (exact) into a dense [N][K] buffer, which the half kernel reads
+__global__ __launch_bounds__(256) void widen_i8_f16(const signed char *__restrict__ q, _Float16 *__restrict__ out,
+                                                    int N, int K, int q_stride) {
+  const size_t n = blockIdx.y, k = ((size_t)blockIdx.x * 256 + threadIdx.x) * 8;
+  if ((int)n >= N || k >= (size_t)K) return;
+  typedef signed char c8 __attribute__((ext_vector_type(8)));
+  const c8 v = *(const c8 *)(q + n * q_stride + k);
+  f16x8 h;
+#pragma unroll
+  for (int i = 0; i < 8; i++) h[i] = (_Float16)v[i];
+  *(f16x8 *)(out + n * K + k) = h;
+}
+
+// Formats: WFMT 1 (q8: int8 A and W, sa[m] sw[n]), 4 (f16: half A and W), 5 (bf16), 6 (h8: half A, int8 W with
+// sw[n]; W widened to half first).
+template <int OT, int EPI, bool HAS_BIAS, int WFMT>
 int launch_gemm(const Pipeline &pl, hipStream_t stream, const Arg *a, int nargs, const void *params,
                 uint32_t params_len, std::string *err) {
   (void)pl;
+  constexpr int AT = WFMT == 1 ? A_I8 : WFMT == 5 ? A_BF16 : A_F16;
+  constexpr int SM = WFMT == 1 ? S_ROW_COL : WFMT == 6 ? S_COL : S_NONE;
+  constexpr int ES = AT == A_I8 ? 1 : 2;             // bytes per A element
+  constexpr int WES = WFMT == 1 || WFMT == 6 ? 1 : 2;  // bytes per W element as given
   if (params_len != sizeof(GemmParams)) {
     *err = "parameter block of " + std::to_string(params_len) + " bytes, expected " +
            std::to_string(sizeof(GemmParams));
@@ -348,11 +399,12 @@ int launch_gemm(const Pipeline &pl, hipStream_t stream, const Arg *a, int nargs,
   }
   GemmParams p;
   memcpy(&p, params, sizeof p);
-  if (p.M < 0 || p.N < 1 || p.K < KS || p.K % KS || p.a_stride < p.K || p.w_stride < p.K || p.c_stride < p.N ||
-      p.a_stride % 16 || p.w_stride % 16) {
+  constexpr int KE = KS / ES;  // K elements per step
+  if (p.M < 0 || p.N < 1 || p.K < KE || p.K % KE || p.a_stride < p.K || p.w_stride < p.K || p.c_stride < p.N ||
+      (p.a_stride * ES) % 16 || (p.w_stride * WES) % (WFMT == 6 ? 8 : 16)) {
     *err = "bad shape: M " + std::to_string(p.M) + " N " + std::to_string(p.N) + " K " + std::to_string(p.K) +
-           " (a multiple of 64) a_stride " + std::to_string(p.a_stride) + " w_stride " +
-           std::to_string(p.w_stride) + " (multiples of 16) c_stride " + std::to_string(p.c_stride);
+           " (a multiple of " + std::to_string(KE) + ") a_stride " + std::to_string(p.a_stride) + " w_stride " +
+           std::to_string(p.w_stride) + " (16-byte rows) c_stride " + std::to_string(p.c_stride);
     return -1;
   }
   if (nargs < (EPI ? 8 : 5)) {
@@ -374,9 +426,9 @@ int launch_gemm(const Pipeline &pl, hipStream_t stream, const Arg *a, int nargs,
   if (p.M == 0) return 0;
   const uint64_t M = p.M, N = p.N;
   constexpr int OSZ = OT == T_F32 ? 4 : 2;
-  if (!need(0, (M - 1) * p.a_stride + p.K, "a") || !need(1, (N - 1) * p.w_stride + p.K, "w") ||
-      !need(2, N * 4, "sw") || !need(3, M * 4, "sa") || !need(4, ((M - 1) * p.c_stride + N) * OSZ, "out") ||
-      (HAS_BIAS && !need(5, N * 4, "bias")))
+  if (!need(0, ((M - 1) * p.a_stride + p.K) * ES, "a") || !need(1, ((N - 1) * p.w_stride + p.K) * WES, "w") ||
+      (SM != S_NONE && !need(2, N * 4, "sw")) || (SM == S_ROW_COL && !need(3, M * 4, "sa")) ||
+      !need(4, ((M - 1) * p.c_stride + N) * OSZ, "out") || (HAS_BIAS && !need(5, N * 4, "bias")))
     return -1;
   int ntypes = 1;
   if (EPI) {
@@ -393,13 +445,24 @@ int launch_gemm(const Pipeline &pl, hipStream_t stream, const Arg *a, int nargs,
       *err = std::string(i ? "w" : "a") + " must be 16-byte aligned";
       return -1;
     }
+  const void *wptr = a[1].ptr;
+  if constexpr (WFMT == 6) {
+    // the widened weights go to the stream's scratch buffer; the product reads them with a dense row stride
+    _Float16 *wh = (_Float16 *)split_workspace(stream, (size_t)N * p.K * 2, "gemm (h8 weights)", err);
+    if (!wh) return -1;
+    hipLaunchKernelGGL(widen_i8_f16, dim3((unsigned)((p.K / 8 + 255) / 256), (unsigned)N), dim3(256), 0, stream,
+                       (const signed char *)a[1].ptr, wh, p.N, p.K, p.w_stride);
+    wptr = wh;
+    p.w_stride = p.K;
+  }
   // 16-byte vector access to the output (and the column vectors) when alignment and N allow it
   constexpr int VE = 16 / OSZ;
   auto al16 = [](const void *q) { return (uintptr_t)q % 16 == 0; };
-  const bool vec = al16(a[4].ptr) && (p.c_stride * OSZ) % 16 == 0 && p.N % VE == 0 && al16(a[2].ptr) &&
-                   (!HAS_BIAS || al16(a[5].ptr)) && (!EPI || (al16(a[7].ptr) && p.g_stride % 4 == 0));
+  const bool vec = al16(a[4].ptr) && (p.c_stride * OSZ) % 16 == 0 && p.N % VE == 0 &&
+                   (SM == S_NONE || al16(a[2].ptr)) && (!HAS_BIAS || al16(a[5].ptr)) &&
+                   (!EPI || (al16(a[7].ptr) && p.g_stride % 4 == 0));
   const int ntm = (p.M + TM - 1) / TM, ntn = (p.N + TN - 1) / TN;
-  auto kern = gemm_q8_kernel<OT, EPI, HAS_BIAS>;
+  auto kern = gemm_kernel<OT, EPI, HAS_BIAS, AT, SM>;
   constexpr int LDS_BYTES =
       std::max(NST * STAGE, OT == T_F32 ? TM / 2 * (TN * 4 + 16) : TM * (TN * 2 + 16));
   static bool attr_set = false;
@@ -411,22 +474,25 @@ int launch_gemm(const Pipeline &pl, hipStream_t stream, const Arg *a, int nargs,
     }
     attr_set = true;
   }
-  hipLaunchKernelGGL(kern, dim3((unsigned)(ntm * ntn)), dim3(NWG * 64), LDS_BYTES, stream,
-                     (const signed char *)a[0].ptr, (const signed char *)a[1].ptr, (const float *)a[2].ptr,
-                     (const float *)a[3].ptr, a[4].ptr, HAS_BIAS ? (const float *)a[5].ptr : nullptr,
-                     EPI ? (const unsigned char *)a[6].ptr : nullptr, EPI ? (const float *)a[7].ptr : nullptr, p, ntm,
-                     ntn, ntypes, vec);
+  hipLaunchKernelGGL(kern, dim3((unsigned)(ntm * ntn)), dim3(NWG * 64), LDS_BYTES, stream, (const char *)a[0].ptr,
+                     (const char *)wptr, SM != S_NONE ? (const float *)a[2].ptr : nullptr,
+                     SM == S_ROW_COL ? (const float *)a[3].ptr : nullptr, a[4].ptr,
+                     HAS_BIAS ? (const float *)a[5].ptr : nullptr, EPI ? (const unsigned char *)a[6].ptr : nullptr,
+                     EPI ? (const float *)a[7].ptr : nullptr, p, ntm, ntn, ntypes, vec);
   return 0;
 }
 
-template <int OT, int EPI>
-LaunchFn pick_bias(bool bias) {
-  return bias ? launch_gemm<OT, EPI, true> : launch_gemm<OT, EPI, false>;
+template <int WFMT>
+LaunchFn pick(int epi, int ot, bool bias) {
+  if (epi) return bias ? launch_gemm<T_F32, 1, true, WFMT> : launch_gemm<T_F32, 1, false, WFMT>;
+  if (ot == T_BF16) return bias ? launch_gemm<T_BF16, 0, true, WFMT> : launch_gemm<T_BF16, 0, false, WFMT>;
+  if (ot == T_F16) return bias ? launch_gemm<T_F16, 0, true, WFMT> : launch_gemm<T_F16, 0, false, WFMT>;
+  return bias ? launch_gemm<T_F32, 0, true, WFMT> : launch_gemm<T_F32, 0, false, WFMT>;
 }
 
 }  // namespace
 
-// Macros (those of h3metal/ops.py:161-164): WFMT (only 1 = Q8 here), EPI (0 or 1), OUT_T (half | bfloat |
+// Macros (those of h3metal/ops.py:161-164): WFMT (1 q8, 4 f16, 5 bf16, 6 h8), EPI (0 or 1), OUT_T (half | bfloat |
 // float; float for EPI 1), HAS_BIAS. The reference's tile and layout choices TM, TN, NSG, G, SWZ, FAST_LAYOUT
 // are accepted and unused (this kernel's tiles are its own); LORA must be 0.
 bool make_gemm(const std::string &fn, const Macros &m, Pipeline *pl, std::string *err) {
@@ -450,8 +516,8 @@ bool make_gemm(const std::string &fn, const Macros &m, Pipeline *pl, std::string
       return false;
     }
   }
-  if (wfmt != 1) {
-    *err = "weight format " + std::to_string(wfmt) + " not built (only WFMT=1, int8 weights and activations)";
+  if (wfmt != 1 && wfmt != 4 && wfmt != 5 && wfmt != 6) {
+    *err = "weight format " + std::to_string(wfmt) + " not built (WFMT 1 q8, 4 f16, 5 bf16, 6 h8)";
     return false;
   }
   if (lora) {
@@ -468,12 +534,10 @@ bool make_gemm(const std::string &fn, const Macros &m, Pipeline *pl, std::string
     *err = "OUT_T must be half|bfloat|float (float with EPI 1)";
     return false;
   }
-  LaunchFn f;
-  if (epi) f = pick_bias<T_F32, 1>(hb != 0);
-  else if (ot == T_BF16) f = pick_bias<T_BF16, 0>(hb != 0);
-  else if (ot == T_F16) f = pick_bias<T_F16, 0>(hb != 0);
-  else f = pick_bias<T_F32, 0>(hb != 0);
-  pl->launch = f;
+  pl->launch = wfmt == 1 ? pick<1>(epi, ot, hb != 0)
+               : wfmt == 4 ? pick<4>(epi, ot, hb != 0)
+               : wfmt == 5 ? pick<5>(epi, ot, hb != 0)
+                           : pick<6>(epi, ot, hb != 0);
   pl->threads = NWG * 64;
   return true;
 }

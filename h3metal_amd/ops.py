@@ -7,7 +7,8 @@ return value (None; results are valid after `gpu.wait()`):
   attention     <- h3metal/ops.py:177-191
   qk_norm_rope  <- h3metal/ops.py:225-239
   rot_q8        <- h3metal/ops.py:214-222 (the consumer of the attention output, h3metal/dit.py:209)
-  QWeight, gemm <- h3metal/ops.py:19-34, 124-174 (the int8 projections around attention; weight format q8)
+  QWeight, gemm <- h3metal/ops.py:19-34, 124-174 (the projections around attention; weight formats q8, h8,
+                   f16, bf16)
   pad_rows      <- h3metal/ops.py:116-117
 
 Element types come from the tensors, as in the reference (`OUT_DT`,
@@ -24,6 +25,7 @@ from .gpu import Gpu, Tensor, pack
 
 OUT_DT = {"f16": "half", "bf16": "bfloat", "f32": "float"}
 FMT_ID = {"q8": 1, "q4": 2, "q4g": 3, "f16": 4, "bf16": 5, "h8": 6, "h4": 7, "h4g": 8}  # h3metal/ops.py:15
+GEMM_ACT = {"q8": "i8", "h8": "f16", "f16": "f16", "bf16": "bf16"}  # the formats built here and their activations
 LOG2E = 1.4426950408889634
 
 
@@ -116,7 +118,8 @@ def rot_q8(gpu: Gpu, x: Tensor, out: Tensor, sa: Tensor | None, M: int, D: int, 
 @dataclass
 class QWeight:
     """A linear layer's weight on the GPU: W[N][K] in one of the reference's formats (h3metal/ops.py:19-34).
-    This build runs the int8 format "q8" (int8 codes W[N][K] row-major, one float scale per output row sw[N])."""
+    This build runs "q8" and "h8" (int8 codes W[N][K] row-major, one float scale per output row sw[N]; int8 or
+    half activations) and "f16" / "bf16" (W[N][K] half / bfloat, no scales)."""
     fmt: str
     w: Tensor
     sw: Tensor | None
@@ -135,18 +138,22 @@ class QWeight:
 def gemm(gpu: Gpu, a: Tensor, wt: QWeight, out: Tensor, M: int, *, sa: Tensor | None = None, epi: int = 0,
          rtype: Tensor | None = None, gate: Tensor | None = None, g_stride: int = 0, c_stride: int | None = None,
          a_stride: int | None = None, tile=(64, 128, 4), swz: int = 1, ksplit: int = 1, _low=None):
-    """out = A x W^T (epi 0), or out += gate[rtype] * (A x W^T) (epi 1, out float), with A int8 [M][K] and its
-    row scales sa, W a q8 QWeight: v[m][n] = sa[m] * sw[n] * (a_m . w_n) (+ bias[n]).
+    """out = A x W^T (epi 0), or out += gate[rtype] * (A x W^T) (epi 1, out float), plus bias[n]:
+      q8:  A int8 [M][K] with row scales sa, W int8 codes, v = sa[m] * sw[n] * (a_m . w_n)
+      h8:  A half, W int8 codes, v = sw[n] * (a_m . w_n)
+      f16 / bf16: A and W half / bfloat, v = a_m . w_n
 
     ksplit: accumulate over that many consecutive slices of K in separate dispatches (epi 1 only), as the
     reference does. tile / swz are the Metal kernel's tile choices: checked as the reference checks them (the
     tile width must divide N) and otherwise unused (the gfx950 kernel uses 256 x 256 tiles and covers any N)."""
-    if wt.fmt != "q8":
-        raise NotImplementedError(f"gemm: weight format {wt.fmt!r} is not built (only q8)")
+    if wt.fmt not in GEMM_ACT:
+        raise NotImplementedError(f"gemm: weight format {wt.fmt!r} is not built (q8, h8, f16, bf16)")
+    if a.dtype != GEMM_ACT[wt.fmt]:
+        raise ValueError(f"gemm: format {wt.fmt} takes {GEMM_ACT[wt.fmt]} activations, got {a.dtype}")
     if wt.low is not None or _low is not None:
         raise NotImplementedError("gemm: low-rank (LoRA) terms are not built")
     if ksplit > 1:
-        if epi != 1 or wt.K % (ksplit * 256):
+        if epi != 1 or wt.fmt not in ("q8", "h8") or wt.K % (ksplit * 256):
             raise ValueError(f"cannot split K of a {wt.fmt} product (epi {epi}, K {wt.K}) {ksplit} ways")
         kp = wt.K // ksplit
         for i in range(ksplit):
@@ -158,7 +165,7 @@ def gemm(gpu: Gpu, a: Tensor, wt: QWeight, out: Tensor, M: int, *, sa: Tensor | 
     tm, tn, nsg = tile
     if wt.N % tn:
         raise ValueError(f"gemm tile {tile}: {tn} columns do not divide the product's {wt.N}")
-    if sa is None:
+    if wt.fmt == "q8" and sa is None:
         raise ValueError("gemm: int8 activations need their row scales sa")
     out_t = OUT_DT[out.dtype] if epi == 0 else "float"
     k = gpu.kernel("gemm", "gemm", WFMT=FMT_ID[wt.fmt], EPI=epi, OUT_T=out_t, TM=tm, TN=tn, NSG=nsg, G=wt.G,

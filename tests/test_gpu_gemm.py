@@ -188,3 +188,105 @@ def test_refusals(gpu):
         ops.gemm(gpu, A, ops.QWeight("q8", wt.w, wt.sw, 256, 200, ws=256), out, 64, sa=SA, a_stride=256)
     with pytest.raises(GpuError):  # the output does not hold M padded rows
         ops.gemm(gpu, A, wt, gpu.empty((32, 256), "f16"), 64, sa=SA)
+
+def float_case(gpu, fmt, rng, M, N, K, bias):
+    """Device operands of an h8 / f16 / bf16 product and its float64 value (before bias and epilogue)."""
+    af = rng.standard_normal((M, K)).astype(np.float32)
+    b = rng.standard_normal(N).astype(np.float32) if bias else None
+    if fmt == "bf16":
+        ab = to_bf16(af)
+        a_dev, a_val = gpu.upload(ab, "bf16"), from_bf16(ab)
+    else:
+        ah = af.astype(np.float16)
+        a_dev, a_val = gpu.upload(ah), ah.astype(np.float32)
+    if fmt == "h8":
+        q = rng.integers(-127, 128, size=(N, K), dtype=np.int8)
+        sw = rng.uniform(0.001, 0.01, size=N).astype(np.float32)
+        wt = ops.QWeight("h8", gpu.upload(q), gpu.upload(sw), N, K, bias=gpu.upload(b) if bias else None)
+        v = og.float_product(a_val, q) * sw[None, :].astype(np.float64)
+    else:
+        wf = (rng.standard_normal((N, K)) * 0.05).astype(np.float32)
+        if fmt == "bf16":
+            wb = to_bf16(wf)
+            w_dev, w_val = gpu.upload(wb, "bf16"), from_bf16(wb)
+        else:
+            wh = wf.astype(np.float16)
+            w_dev, w_val = gpu.upload(wh), wh.astype(np.float32)
+        wt = ops.QWeight(fmt, w_dev, None, N, K, bias=gpu.upload(b) if bias else None)
+        v = og.float_product(a_val, w_val)
+    if bias:
+        v = v + b[None, :].astype(np.float64)
+    return a_dev, wt, v
+
+
+@pytest.mark.parametrize("fmt", ["h8", "f16", "bf16"])
+@pytest.mark.parametrize("M,N,K,out_dtype,bias", [(200, 256, 512, "f16", False), (300, 640, 384, "f32", True),
+                                                  (70, 198, 96, "bf16", True), (513, 512, 1280, "f32", False)])
+def test_float_formats_reference_tolerance(gpu, fmt, M, N, K, out_dtype, bias):
+    """h8 / f16 / bf16 products (WFMT 6 / 4 / 5) within the reference's check() tolerance (tests/test_gemm.py:
+    20-84): max error below 2e-3 of the largest output, 1e-2 for bfloat outputs; ragged N and a K of three
+    32-element steps included."""
+    rng = np.random.default_rng(M + N + K + len(fmt))
+    print(f"[gemm {fmt}] M={M} N={N} K={K} out={out_dtype} bias={bias}", flush=True)
+    A, wt, v = float_case(gpu, fmt, rng, M, N, K, bias)
+    out = gpu.empty((M, N), out_dtype)
+    ops.gemm(gpu, A, wt, out, M, tile=(1, 2, 4))
+    gpu.wait()
+    got = out.numpy()
+    got = from_bf16(got).astype(np.float64) if out_dtype == "bf16" else got.astype(np.float64)
+    err = np.abs(got - v).max() / np.abs(v).max()
+    assert err < (2e-3 if out_dtype != "bf16" else 1e-2), err
+
+
+@pytest.mark.parametrize("fmt", ["h8", "f16", "bf16"])
+def test_float_formats_residual_and_k_split(gpu, fmt):
+    """epi 1 with row types and gates; h8 also with K split over dispatches (the reference allows it for h8)."""
+    rng = np.random.default_rng(7)
+    M, N, K = 256, 512, 1024
+    A, wt, v = float_case(gpu, fmt, rng, M, N, K, True)
+    x0 = rng.standard_normal((M, N)).astype(np.float32)
+    types = rng.integers(0, 3, size=M).astype(np.uint8)
+    gates = rng.standard_normal((3, N)).astype(np.float32)
+    want = x0.astype(np.float64) + gates[types].astype(np.float64) * v
+    for ksplit in ((1, 4) if fmt == "h8" else (1,)):
+        X = gpu.upload(x0)
+        ops.gemm(gpu, A, wt, X, M, epi=1, rtype=gpu.upload(types), gate=gpu.upload(gates), ksplit=ksplit,
+                 tile=(64, 256, 8))
+        gpu.wait()
+        err = np.abs(X.numpy().astype(np.float64) - want).max() / np.abs(want).max()
+        assert err < 2e-3, (fmt, ksplit, err)
+
+
+def test_rotated_half_output_into_h8_projection(gpu):
+    """The text encoder's chain (h3metal/te.py:195-196): rot_q8 with out_hr (rotated rows in half precision)
+    feeding an h8 projection; against float64 of the rotated rows."""
+    from oracle import rot_q8 as orq
+    rng = np.random.default_rng(8)
+    M, D, N = 96, 1024, 512
+    xb = to_bf16((rng.standard_normal((M, D)) * 2).astype(np.float32))
+    X = gpu.upload(xb, "bf16")
+    hr = gpu.empty((M, D), "f16")
+    ops.rot_q8(gpu, X, hr, None, M, D, out_hr=True)
+    q = rng.integers(-127, 128, size=(N, D), dtype=np.int8)
+    sw = rng.uniform(0.001, 0.01, size=N).astype(np.float32)
+    wt = ops.QWeight("h8", gpu.upload(q), gpu.upload(sw), N, D)
+    out = gpu.empty((M, N), "f32")
+    ops.gemm(gpu, hr, wt, out, M, tile=(1, 2, 4))
+    gpu.wait()
+    _, _, r = orq.rot_q8(from_bf16(xb), D)
+    want = og.float_product(r.astype(np.float16).astype(np.float32), q) * sw[None, :].astype(np.float64)
+    err = np.abs(out.numpy() - want).max() / np.abs(want).max()
+    assert err < 2e-3, err
+
+
+def test_float_format_refusals(gpu):
+    rng = np.random.default_rng(9)
+    A, wt, _ = float_case(gpu, "f16", rng, 64, 256, 256, False)
+    out = gpu.empty((64, 256), "f16")
+    with pytest.raises(ValueError):  # f16 weights take half activations
+        ops.gemm(gpu, gpu.upload(np.zeros((64, 256), np.int8)), wt, out, 64, tile=(1, 2, 4))
+    with pytest.raises(ValueError):  # the reference splits K only for integer-weight formats
+        ops.gemm(gpu, A, wt, gpu.empty((64, 256), "f32"), 64, epi=1, rtype=gpu.upload(np.zeros(64, np.uint8)),
+                 gate=gpu.upload(np.ones((1, 256), np.float32)), ksplit=2, tile=(1, 2, 4))
+    with pytest.raises(GpuError):  # K must be a multiple of 32 for 16-bit operands
+        ops.gemm(gpu, A, ops.QWeight("f16", wt.w, None, 256, 200, ws=256), out, 64, a_stride=256, tile=(1, 2, 4))

@@ -346,3 +346,15 @@ def test_gemm_epilogue_order_and_exact_cases():
     got = og.residual(x, vv, gate, rt)
     np.testing.assert_allclose(got, x.astype(np.float64) + gate[rt].astype(np.float64) * vv, rtol=1e-6, atol=1e-6)
     assert got[0, 0] == np.float32(x[0, 0] + np.float32(gate[rt[0], 0] * vv[0, 0]))
+
+
+def test_gemm_float_product_brute_force():
+    """float_product against Python sums of exactly representable half values (small integers and halves), so
+    every product and partial sum is exact in float64."""
+    from oracle import gemm as og
+    rng = np.random.default_rng(6)
+    a = (rng.integers(-64, 65, size=(5, 40)) / 2.0).astype(np.float16)
+    w = rng.integers(-127, 128, size=(7, 40), dtype=np.int8)
+    got = og.float_product(a.astype(np.float32), w)
+    want = np.array([[sum(float(a[i, k]) * int(w[j, k]) for k in range(40)) for j in range(7)] for i in range(5)])
+    assert np.array_equal(got, want)
