@@ -67,8 +67,10 @@ void *h3_buffer_device(void *buf);
 
 // Looks up kernel `fn` of module `file` specialised by macros "NAME=value;...".
 // Modules: "attention" (fn "attention", "attention_scores") and "ops" (fn
-// "qk_norm_rope", "rot_q8") and "gemm" (fn "gemm"); the reference's "attention.metal"/"ops.metal" names are also
-// accepted. NULL (with h3_last_error) for an unknown kernel or an unsupported
+// "qk_norm_rope", "rot_q8") and "gemm" (fn "gemm"; macro WFMT selects the weight
+// format as in kernels/gemm.metal:1-40: 1 q8, 4 f16, 5 bf16, 6 h8; other formats
+// return NULL); the reference's "attention.metal"/"ops.metal"/"gemm.metal" names are
+// also accepted. NULL (with h3_last_error) for an unknown kernel or an unsupported
 // specialisation. The handle is owned by the context. Reference: src/capi.h:54-57.
 void *h3_pipeline(h3_ctx *ctx, const char *file, const char *fn, const char *macros);
 int h3_pipeline_max_threads(void *pso);
