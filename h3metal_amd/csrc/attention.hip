@@ -410,8 +410,19 @@ __global__ __launch_bounds__(NW * 64) void attention_kernel(const char *__restri
       return;
     }
     const int kb = j * BK;
-    float x[2][16];
-    // element i of lane-half hl holds key kb + 32 t + 16 (i / 8) + 8 hl + i % 8
+    // x: the scores in log2 units before the query scale. Element i of lane-half hl holds key
+    // kb + 32 t + 16 (i / 8) + 8 hl + i % 8.
+    auto mask_tile = [&](f32x16 &v, int t) __attribute__((always_inline)) {
+#pragma unroll
+      for (int i = 0; i < 16; i++) {
+        const int key = kb + 32 * t + 16 * (i >> 3) + 8 * hl + (i & 7);
+        bool masked = key >= Lk;
+        if constexpr (CAUSAL) masked = masked || key > q + p.causal_off;
+        if (masked) v[i] = -INFINITY;
+      }
+    };
+    const bool tail = CAUSAL || kb + BK > Lk;
+    f32x16 x[2];
     if constexpr (C::QK8) {
       const float *ksc = (const float *)(smem + C::SOFF) + (j % 3) * BK;
       // all key scales of the block first: one LDS round trip instead of one per group of four keys
@@ -428,7 +439,7 @@ __global__ __launch_bounds__(NW * 64) void attention_kernel(const char *__restri
 #pragma unroll
       for (int t = 0; t < 2; t++) {
         // bit-cast the whole tile (per-element casts of an MFMA result have been miscompiled into a splat)
-        const f32x16 sf = __builtin_bit_cast(f32x16, s[t]);
+        x[t] = __builtin_bit_cast(f32x16, s[t]);
 #pragma unroll
         for (int s8 = 0; s8 < 2; s8++)
 #pragma unroll
@@ -436,25 +447,22 @@ __global__ __launch_bounds__(NW * 64) void attention_kernel(const char *__restri
 #pragma unroll
             for (int e = 0; e < 4; e++) {
               const int i = 8 * s8 + 4 * hh + e;
-              x[t][i] = (sf[i] - MAGICF) * k4[t][s8][hh][e];
+              x[t][i] = (x[t][i] - MAGICF) * k4[t][s8][hh][e];
             }
       }
+      if (tail) {
+#pragma unroll
+        for (int t = 0; t < 2; t++) mask_tile(x[t], t);
+      }
     } else {
+      // 16-bit scores are masked in their accumulators (a copy into x before the branch would be made at
+      // every block)
+      if (tail) {
 #pragma unroll
-      for (int t = 0; t < 2; t++)
+        for (int t = 0; t < 2; t++) mask_tile(s[t], t);
+      }
 #pragma unroll
-        for (int i = 0; i < 16; i++) x[t][i] = s[t][i];
-    }
-    if (CAUSAL || kb + BK > Lk) {
-#pragma unroll
-      for (int t = 0; t < 2; t++)
-#pragma unroll
-        for (int i = 0; i < 16; i++) {
-          const int key = kb + 32 * t + 16 * (i >> 3) + 8 * hl + (i & 7);
-          bool masked = key >= Lk;
-          if constexpr (CAUSAL) masked = masked || key > q + p.causal_off;
-          if (masked) x[t][i] = -INFINITY;
-        }
+      for (int t = 0; t < 2; t++) x[t] = s[t];
     }
     float am[2] = {-INFINITY, -INFINITY};  // two independent chains
 #pragma unroll
