@@ -361,20 +361,43 @@ __global__ __launch_bounds__(NW * 64) void attention_kernel(const char *__restri
     i16x8 va[2][D / 32];
     if (j < nblk) {
       const char *Ks = smem + C::KOFF + (j & 1) * C::KBYTES;
-      i32x4 ka[2][C::NCH];
-#pragma unroll
-      for (int t = 0; t < 2; t++) {
+      auto kload = [&](int t, int c) {
         const int key = 32 * t + krow;
-        const char *kp = Ks + key * C::RB;
-        const int sw = kswz<C::RB, C::NP>(key);
+        return *(const i32x4 *)(Ks + key * C::RB + (((2 * c + hl) ^ kswz<C::RB, C::NP>(key)) * 16));
+      };
+      if constexpr (C::NCH <= 4) {
+        // int8 rows (4 chunks): every K operand at once
+        i32x4 ka[2][C::NCH];
 #pragma unroll
-        for (int c = 0; c < C::NCH; c++) ka[t][c] = *(const i32x4 *)(kp + (((2 * c + hl) ^ sw) * 16));
+        for (int t = 0; t < 2; t++)
+#pragma unroll
+          for (int c = 0; c < C::NCH; c++) ka[t][c] = kload(t, c);
+        if (do_pv) vload(0, va[0]);
+#pragma unroll
+        for (int t = 0; t < 2; t++)
+#pragma unroll
+          for (int c = 0; c < C::NCH; c++) s[t] = mma_qk<QKT>(ka[t][c], qreg[c], c == 0 ? sinit : s[t]);
+      } else {
+        // 16-bit rows (8 chunks): the operands of chunk c + 2 are read while chunk c multiplies (a 3-deep
+        // ring; reading all 16 at once leaves too few registers, and the compiler then waits on each one)
+        i32x4 ka[3][2];
+#pragma unroll
+        for (int c = 0; c < 2; c++)
+#pragma unroll
+          for (int t = 0; t < 2; t++) ka[c][t] = kload(t, c);
+        if (do_pv) vload(0, va[0]);
+#pragma unroll
+        for (int c = 0; c < C::NCH; c++) {
+          if (c + 2 < C::NCH) {
+#pragma unroll
+            for (int t = 0; t < 2; t++) ka[(c + 2) % 3][t] = kload(t, c + 2);
+          }
+          // keep the reads here (the scheduler would sink each one to its MFMA and expose its latency)
+          __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+          for (int t = 0; t < 2; t++) s[t] = mma_qk<QKT>(ka[c % 3][t], qreg[c], c == 0 ? sinit : s[t]);
+        }
       }
-      if (do_pv) vload(0, va[0]);
-#pragma unroll
-      for (int t = 0; t < 2; t++)
-#pragma unroll
-        for (int c = 0; c < C::NCH; c++) s[t] = mma_qk<QKT>(ka[t][c], qreg[c], c == 0 ? sinit : s[t]);
     } else if (do_pv) {
       vload(0, va[0]);
     }
