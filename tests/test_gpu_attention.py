@@ -468,3 +468,45 @@ def test_tail_split_matches_whole_tiles(gpu, q8_path):
         assert err.max() < NS_MAX and err.mean() < NS_MEAN, (err.max(), err.mean())
     assert np.abs(outs[0] - outs[1]).max() < 2e-3
     assert (outs[0][Lq:] == 0).all()
+
+
+@pytest.mark.parametrize("H,KVH,Lq,L,seq", [(4, 4, 1000, 1500, None), (6, 2, 777, 2049, None), (4, 4, 300, 700, 2)])
+def test_int8_three_group_kernel_matches_ping_pong(gpu, H, KVH, Lq, L, seq):
+    """int8 scores at D=128 without a causal mask run on the three-group kernel (GROUPS=3, the default); GROUPS=2
+    keeps them on the two-group ping-pong kernel. Same inputs through both, with and without the tail split:
+    every output meets the tolerance against float64 and the kernels agree to rounding. Ragged L (a partly masked
+    last key block), GQA, several 384-row query blocks per head and batched sequences (seq_heads) included."""
+    rng = np.random.default_rng(H * 1000 + L)
+    D = 128
+    qr, kr = -(-Lq // 512) * 512, -(-L // 64) * 64 + 64
+    qi, qs = q8(rng.standard_normal((H, Lq, D)).astype(np.float32))
+    ki, ks = q8(rng.standard_normal((KVH, L, D)).astype(np.float32))
+    v = to_bf16(rng.standard_normal((KVH, L, D)).astype(np.float32))
+    Q, K, V = padded(gpu, qi, qr, "i8"), padded(gpu, ki, kr, "i8"), padded(gpu, v, kr, "bf16")
+    extra = dict(q_scale=padded(gpu, qs, qr, "f32"), k_scale=padded(gpu, ks, kr, "f32"))
+    seq_heads = seq or H
+    nseq = H // seq_heads
+    outs = []
+    for groups, split in ((3, 1), (3, 0), (2, 1)):
+        print(f"[attention] groups={groups} split={split} H={H} KVH={KVH} Lq={Lq} L={L} seq={seq}", flush=True)
+        O = gpu.empty((nseq * qr, seq_heads * D), "f32")
+        ops.attention(gpu, Q, K, V, O, Lq=Lq, L=L, H=H, KVH=KVH, D=D, q_rows=qr, k_rows=kr, scale=D ** -0.5,
+                      seq_heads=seq_heads, seq_rows=qr, GROUPS=groups, SPLIT=split, **extra)
+        gpu.wait()
+        outs.append(O.numpy().astype(np.float64))
+    rq = qi * qs[..., None].astype(np.float64)
+    rk = ki * ks[..., None].astype(np.float64)
+    ref = oa.ref_attention(rq, rk, from_bf16(v), D ** -0.5)  # [Lq][H * D]
+    for o in outs:
+        got = np.concatenate([o[s * qr:s * qr + Lq, :] for s in range(nseq)], axis=1)
+        err = np.abs(got - ref)
+        assert err.max() < NS_MAX and err.mean() < NS_MEAN, (err.max(), err.mean())
+    assert np.abs(outs[0] - outs[2]).max() < 2e-3
+    assert np.abs(outs[1] - outs[2]).max() < 2e-3
+
+
+def test_groups_macro_refused(gpu):
+    """GROUPS accepts 2 or 3 only (checked on the host when the pipeline is made)."""
+    from h3metal_amd.gpu import GpuError
+    with pytest.raises(GpuError, match="GROUPS"):
+        gpu.kernel("attention", "attention", HD=128, QK8=1, IN_T="bfloat", O_T="bfloat", GROUPS=4)
