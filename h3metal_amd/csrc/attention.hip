@@ -743,17 +743,11 @@ __global__ __launch_bounds__(NW3 * 64) void attention3_kernel(const char *__rest
   // matrix phase of block j: O^T += V(j-1)^T P(j-1)^T, then S(j) = K(j) Q^T (P V first: the scores' registers
   // are free until then)
   auto matrix_phase = [&](int j) {
-    unsigned vb[D / 32], kb4[C::NCH];
 #pragma unroll
-    for (int db = 0; db < D / 32; db++) {
-      vb[db] = vbase[db];
-      asm volatile("" : "+v"(vb[db]));
-    }
+    for (int db = 0; db < D / 32; db++) asm volatile("" : "+v"(vbase[db]));
 #pragma unroll
-    for (int c = 0; c < C::NCH; c++) {
-      kb4[c] = kbase[c];
-      asm volatile("" : "+v"(kb4[c]));
-    }
+    for (int c = 0; c < C::NCH; c++) asm volatile("" : "+v"(kbase[c]));
+    const unsigned *vb = vbase, *kb4 = kbase;
     if (j >= 1) {
       const char *Vs = smem + C::VOFF + ((j - 1) % 3) * C::VBYTES;
       auto vload = [&](int st, i16x8 (&va)[D / 32]) {
