@@ -602,15 +602,6 @@ __global__ __launch_bounds__(NW * 64) void attention_kernel(const char *__restri
 // the first reader (group 0's matrix phase of block j + 2, slot 3j + 6).
 constexpr int NW3 = 12;
 
-__device__ __forceinline__ void dma_b128(unsigned m0, unsigned voff, __amdgpu_buffer_rsrc_t r) {
-  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds" ::"s"(m0), "v"(voff), "s"(r)
-               : "memory", "m0");
-}
-__device__ __forceinline__ void dma_b32(unsigned m0, unsigned voff, __amdgpu_buffer_rsrc_t r) {
-  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dword %1, %2, 0 offen lds" ::"s"(m0), "v"(voff), "s"(r)
-               : "memory", "m0");
-}
-
 struct Cfg3 {
   static constexpr int D = 128, RB = 128, NP = 8, NCH = 4;
   static constexpr int NT = NW3 * 64, BQ = NW3 * 32;
@@ -697,14 +688,14 @@ __global__ __launch_bounds__(NW3 * 64) void attention3_kernel(const char *__rest
     const __amdgpu_buffer_rsrc_t r = rsrc(Kh, blk, C::RB);
 #pragma unroll
     for (int rr = 0; rr < 2; rr++)
-      dma_b128(lds0 + C::KOFF + (blk % 3) * C::KBYTES + (rr * 4 + wl) * 1024, goff[rr], r);
-    if (wl == 0) dma_b32(lds0 + C::SOFF + (blk & 3) * BK * 4, lane * 4, rsrc(ksh, blk, 4));
+      dma16(lds0 + C::KOFF + (blk % 3) * C::KBYTES + (rr * 4 + wl) * 1024, goff[rr], r);
+    if (wl == 0) dma4(lds0 + C::SOFF + (blk & 3) * BK * 4, lane * 4, rsrc(ksh, blk, 4));
   };
   auto stage_v = [&](int blk) {  // groups 1, 2: their half of V of block blk
     const __amdgpu_buffer_rsrc_t r = rsrc(Vh, blk, D * 2);
 #pragma unroll
     for (int rr = 0; rr < 2; rr++)
-      dma_b128(lds0 + C::VOFF + (blk % 3) * C::VBYTES + (grp - 1) * 8192 + (rr * 4 + wl) * 1024, goff[rr], r);
+      dma16(lds0 + C::VOFF + (blk % 3) * C::VBYTES + (grp - 1) * 8192 + (rr * 4 + wl) * 1024, goff[rr], r);
   };
 
   f32x16 o[D / 32];

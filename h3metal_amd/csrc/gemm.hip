@@ -72,13 +72,6 @@ constexpr int STAGE = (TM + TN) * KS;            // LDS bytes per stage
 // 16-byte piece p of LDS row r (64 bytes) sits at slot p ^ ((r / 4) % 4)
 __device__ __forceinline__ int swz(int row, int piece) { return row * KS + ((piece ^ ((row >> 2) & 3)) << 4); }
 
-// LDS-direct 16-byte buffer load: lane i's bytes land at LDS byte m0 + 16 i (offsets beyond the descriptor's
-// range read as zero). Written as assembly so that the compiler does not make every LDS read wait for all of
-// them; the kernel waits itself (vmcnt) before the barrier that publishes a stage.
-__device__ __forceinline__ void dma16(unsigned m0, int voff, __amdgpu_buffer_rsrc_t r) {
-  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds" ::"s"(m0), "v"(voff), "s"(r)
-               : "memory", "m0");
-}
 
 template <int OT>
 __device__ __forceinline__ void store_out(char *p, float v) {
@@ -138,10 +131,10 @@ __global__ __launch_bounds__(NWG * 64) __attribute__((amdgpu_waves_per_eu(2))) v
     const bool ok = kt < nk;
 #pragma unroll
     for (int q = 0; q < NQA; q++)
-      dma16(st + (16 * (NQA * w + q)) * KS, ok ? offa[q] + kt * KS : (int)0x80000000u, ra);
+      dma16(st + (16 * (NQA * w + q)) * KS, ok ? (unsigned)(offa[q] + kt * KS) : 0x80000000u, ra);
 #pragma unroll
     for (int q = 0; q < NQW; q++)
-      dma16(st + (TM + 16 * (NQW * w + q)) * KS, ok ? offw[q] + kt * KS : (int)0x80000000u, rw);
+      dma16(st + (TM + 16 * (NQW * w + q)) * KS, ok ? (unsigned)(offw[q] + kt * KS) : 0x80000000u, rw);
   };
 
   AccOf<AT> acc[MI][NJ];

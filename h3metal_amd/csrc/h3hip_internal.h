@@ -130,6 +130,19 @@ __device__ __forceinline__ void hadamard_lane_stage(float (&v)[N], float c) {
   }
 }
 
+// LDS-direct buffer loads: lane i's 16 (dma16) or 4 (dma4) bytes land at LDS byte m0 + 16 i (+ 4 i); offsets
+// beyond the descriptor's range read as zero. Written as assembly so that the compiler does not make every LDS
+// read wait for them; the caller waits itself (vmcnt) before the barrier that publishes the data. M0 must be
+// wave-uniform; the s_nop gives the load the wait state it needs after the M0 write.
+__device__ __forceinline__ void dma16(unsigned m0, unsigned voff, __amdgpu_buffer_rsrc_t r) {
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds" ::"s"(m0), "v"(voff), "s"(r)
+               : "memory", "m0");
+}
+__device__ __forceinline__ void dma4(unsigned m0, unsigned voff, __amdgpu_buffer_rsrc_t r) {
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dword %1, %2, 0 offen lds" ::"s"(m0), "v"(voff), "s"(r)
+               : "memory", "m0");
+}
+
 // Compute units of the current device (0 if unknown), and the per-stream scratch buffer of the tail splits
 // (at least `bytes`, grown on demand, kept until the process ends; NULL with a message on failure).
 int cu_count();
