@@ -1179,7 +1179,8 @@ bool make_attention(const std::string &fn, const Macros &m, Pipeline *pl, std::s
   else if (hd == 96) f = dump ? pick_types<96, true>(qkt, it, ot, causal) : pick_types<96, false>(qkt, it, ot, causal);
   else f = dump ? pick_types<64, true>(qkt, it, ot, causal) : pick_types<64, false>(qkt, it, ot, causal);
   pl->launch = f;
-  pl->threads = NW * 64;
+  // workgroup size of the kernel the pipeline launches (the three-group kernel: int8, HD 128, no causal mask)
+  pl->threads = (groups == 3 && qk8 && hd == 128 && !causal && !dump) ? NW3 * 64 : NW * 64;
   pl->ival[0] = split != 0;
   pl->ival[1] = groups == 3;
   return true;

@@ -41,7 +41,9 @@ def test_unknown_kernel_and_macros(gpu):
         gpu.kernel("ops", "qk_norm_rope", QKROT=1)
     # the reference's file names and tuning macros are accepted
     k = gpu.kernel("attention.metal", "attention", HD=128, WM=10, BK=32, DB=1, PVORDER=1, VX=1, QK8=1, O_T="bfloat")
-    assert k.max_threads > 0
+    assert k.max_threads == 768  # the three-group kernel's workgroup
+    assert gpu.kernel("attention", "attention", HD=128, QK8=1, O_T="bfloat", GROUPS=2).max_threads == 512
+    assert gpu.kernel("attention", "attention", HD=128, QK8=1, O_T="bfloat", CAUSAL=1).max_threads == 512
 
 
 def test_dispatch_validation(gpu):
