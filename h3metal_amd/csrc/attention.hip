@@ -591,11 +591,12 @@ __global__ __launch_bounds__(NW * 64) void attention_kernel(const char *__restri
 
 // ---------------------------------------------------------------------------------------------------------------
 // Three-group variant for int8 scores, D = 128, no causal mask: 12 waves, three groups of 4 (waves w, w + 4,
-// w + 8 share a SIMD), 384 query rows per workgroup. Each key block is three slots separated by barriers; group g
-// runs its matrix phase (P V of block j-1, then the scores of block j) in slot 3j + g and its vector phase in the
-// two slots after it (conversion, maximum and lazy rescale; then P and the row sums). At any time one wave of a
-// SIMD issues MFMAs and two issue softmax VALU work, so the VALU pipe, which a single wave keeps only partly busy
-// (dependent instructions, exponential latency), is fed from two instruction streams.
+// w + 8: the waves of a workgroup are placed on the 4 SIMDs in turn, so each SIMD holds one wave of each group),
+// 384 query rows per workgroup. Each key block is three slots separated by barriers; group g runs its matrix
+// phase (P V of block j-1, then the scores of block j) in slot 3j + g and its vector phase in the two slots after
+// it (conversion, maximum and lazy rescale; then P and the row sums). At any time one wave of a SIMD issues MFMAs
+// and two issue softmax VALU work, so the VALU pipe is fed from two instruction streams instead of one (measured
+// about 1% faster than the two-group kernel at config 4; the matrix slot is the longer one).
 // Staging is LDS-direct (buffer_load ... lds, no registers): in slot 3j + g, group 0 loads K and the key scales of
 // block j + 2, groups 1 and 2 the two halves of V of block j + 1, into 3-deep rings (scales 4-deep); a wave waits
 // for its loads at the start of its next matrix phase, and the barrier ending that slot publishes them before
