@@ -199,3 +199,50 @@ def test_lds_swizzles_cover_all_banks():
                     addr = voff(8 * h + (l16 >> 2), (db * 32 + (l32 & 16)) // 8, D) + (l16 & 3) * 8
                     banks += [(addr // 4 + i) % 64 for i in range(2)]
                 assert sorted(banks) == list(range(64))
+
+
+def test_three_group_lds_direct_staging_layout():
+    """The three-group attention kernel (csrc/attention.hip, attention3_kernel) stages K and V with LDS-direct
+    loads: lane i of a load instruction writes LDS bytes m0 + 16 i .. + 15, so each lane must fetch the global
+    piece that belongs at that swizzled position. Restated here: over a block's load instructions the written
+    LDS bytes cover the K (8 KB) and V (16 KB) ring slots exactly once, and the piece that lands at each position
+    is the one the operand reads (kswz / voff placement) expect there."""
+    RB, D = 128, 128
+
+    def kswz(key):
+        return (key // 2) % 8
+
+    def voff(key, pc):
+        return key * 256 + ((pc >> 1) ^ (2 * (key & 3))) * 32 + (pc & 1) * 16
+
+    # K: group 0, wave wl, round r: LDS chunk c = 4 r + wl of 1 KB
+    k_written = {}
+    for wl in range(4):
+        for r in range(2):
+            c = r * 4 + wl
+            for lane in range(64):
+                o = c * 1024 + 16 * lane
+                row, slot = o >> 7, (o >> 4) & 7
+                goff = row * RB + (slot ^ kswz(row)) * 16
+                assert o not in k_written
+                k_written[o] = goff
+    assert sorted(k_written) == [16 * i for i in range(512)]
+    for key in range(64):  # the read side: piece p of row key sits at key * RB + (p ^ kswz(key)) * 16
+        for p in range(8):
+            assert k_written[key * RB + ((p ^ kswz(key)) * 16)] == key * RB + p * 16
+    # V: groups 1 and 2 (half = group - 1), wave wl, round r
+    v_written = {}
+    for half in range(2):
+        for wl in range(4):
+            for r in range(2):
+                c = r * 4 + wl
+                for lane in range(64):
+                    o = half * 8192 + c * 1024 + 16 * lane
+                    row, uu, sub = o >> 8, (o & 255) >> 5, (o >> 4) & 1
+                    goff = row * (D * 2) + (2 * (uu ^ (2 * (row & 3))) + sub) * 16
+                    assert o not in v_written
+                    v_written[o] = goff
+    assert sorted(v_written) == [16 * i for i in range(1024)]
+    for key in range(64):
+        for pc in range(16):
+            assert v_written[voff(key, pc)] == key * (D * 2) + pc * 16
