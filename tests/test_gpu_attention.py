@@ -510,3 +510,28 @@ def test_groups_macro_refused(gpu):
     from h3metal_amd.gpu import GpuError
     with pytest.raises(GpuError, match="GROUPS"):
         gpu.kernel("attention", "attention", HD=128, QK8=1, IN_T="bfloat", O_T="bfloat", GROUPS=4)
+
+
+@pytest.mark.parametrize("Lq,L", [(1, 1), (5, 63), (384, 64), (385, 65), (17, 129), (700, 191)])
+def test_int8_three_group_kernel_edges(gpu, Lq, L):
+    """Edge shapes through the three-group kernel (int8, D=128, no causal mask): one query or one key, key counts
+    around the 64-key block (the last block's rows past L load as zeros and are masked), query counts around the
+    384-row tile. Checked against float64 within the north-star tolerance."""
+    rng = np.random.default_rng(Lq * 1000 + L)
+    H, D = 2, 128
+    qr, kr = -(-Lq // 384) * 384, -(-L // 64) * 64
+    qi, qs = q8(rng.standard_normal((H, Lq, D)).astype(np.float32))
+    ki, ks = q8(rng.standard_normal((H, L, D)).astype(np.float32))
+    v = to_bf16(rng.standard_normal((H, L, D)).astype(np.float32))
+    Q, K, V = padded(gpu, qi, qr, "i8"), padded(gpu, ki, kr, "i8"), padded(gpu, v, kr, "bf16")
+    O = gpu.empty((qr, H * D), "f32")
+    print(f"[attention] three-group edge Lq={Lq} L={L}", flush=True)
+    ops.attention(gpu, Q, K, V, O, Lq=Lq, L=L, H=H, KVH=H, D=D, q_rows=qr, k_rows=kr, scale=D ** -0.5,
+                  q_scale=padded(gpu, qs, qr, "f32"), k_scale=padded(gpu, ks, kr, "f32"))
+    gpu.wait()
+    got = O.numpy().astype(np.float64)
+    ref = oa.ref_attention(qi * qs[..., None].astype(np.float64), ki * ks[..., None].astype(np.float64),
+                           from_bf16(v), D ** -0.5)
+    err = np.abs(got[:Lq] - ref)
+    assert err.max() < NS_MAX and err.mean() < NS_MEAN, (err.max(), err.mean())
+    assert (got[Lq:] == 0).all()
