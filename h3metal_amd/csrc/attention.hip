@@ -611,7 +611,8 @@ struct Cfg3 {
   static constexpr int LDS = SOFF + 4 * BK * 4;
 };
 
-template <int VT, int OT>
+// DUMP: instead of attention, write this kernel's raw int32 score accumulators S[h][q][key], for tests.
+template <int VT, int OT, bool DUMP>
 __global__ __launch_bounds__(NW3 * 64) void attention3_kernel(const char *__restrict__ Q, const char *__restrict__ K,
                                                               const char *__restrict__ V, char *__restrict__ O,
                                                               const float *__restrict__ qs,
@@ -780,6 +781,19 @@ __global__ __launch_bounds__(NW3 * 64) void attention3_kernel(const char *__rest
   auto vector_a = [&](int j) {
     if (j >= nblk) return;
     const int kb = j * BK;
+    if constexpr (DUMP) {
+      // element i of lane-half hl holds key 64 j + 32 t + 16 (i / 8) + 8 hl + i % 8
+      if (qvalid) {
+#pragma unroll
+        for (int t = 0; t < 2; t++)
+#pragma unroll
+          for (int i = 0; i < 16; i++) {
+            const int key = kb + 32 * t + 16 * (i >> 3) + 8 * hl + (i & 7);
+            if (key < p.L) *((int *)O + ((size_t)h * p.Lq + q) * p.L + key) = s[t][i];
+          }
+      }
+      return;
+    }
     const float *ksc = (const float *)(smem + C::SOFF) + (j & 3) * BK;
     float am[2];
 #pragma unroll
@@ -827,7 +841,7 @@ __global__ __launch_bounds__(NW3 * 64) void attention3_kernel(const char *__rest
   };
   // second vector slot: P(j) = 2^(x qsc - m), rounded to the value type, and the row sums of the rounded P
   auto vector_b = [&](int j) {
-    if (j >= nblk) return;
+    if (DUMP || j >= nblk) return;
     const float nm = m == -INFINITY ? 0.0f : -m;
     float ls[2] = {0.0f, 0.0f};
 #pragma unroll
@@ -871,6 +885,7 @@ __global__ __launch_bounds__(NW3 * 64) void attention3_kernel(const char *__rest
   }
   for (int i = grp; i < 2; i++) __syncthreads();
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // loads past the last block (zeros) land before the exit
+  if constexpr (DUMP) return;
 
   const float lt = l + __shfl_xor(l, 32);
   if (unit >= 0) {
@@ -1023,7 +1038,7 @@ int launch_attention(const Pipeline &pl, hipStream_t stream, const Arg *args, in
   }
   if (p.Lq == 0) return 0;
   // int8 scores, D = 128, no causal mask: the three-group kernel (unless GROUPS=2)
-  constexpr bool CAN3 = QKT == T_I8 && !CAUSAL && !DUMP && D == 128;
+  constexpr bool CAN3 = QKT == T_I8 && !CAUSAL && D == 128;
   const bool use3 = CAN3 && pl.ival[1];
   const int BQ = use3 ? Cfg3::BQ : C::BQ;
   const int nqb = (p.Lq + BQ - 1) / BQ;
@@ -1053,7 +1068,7 @@ int launch_attention(const Pipeline &pl, hipStream_t stream, const Arg *args, in
   const long ngroups = sp.s ? (long)sp.nfull + (ntiles - sp.nfull) * sp.s : ntiles;
   if constexpr (CAN3) {
     if (use3) {
-      auto kern3 = attention3_kernel<VT, OT>;
+      auto kern3 = attention3_kernel<VT, OT, DUMP>;
       static bool attr3_set = false;
       if (!attr3_set) {
         hipError_t e = hipFuncSetAttribute((const void *)kern3, hipFuncAttributeMaxDynamicSharedMemorySize, Cfg3::LDS);
@@ -1181,7 +1196,7 @@ bool make_attention(const std::string &fn, const Macros &m, Pipeline *pl, std::s
   else f = dump ? pick_types<64, true>(qkt, it, ot, causal) : pick_types<64, false>(qkt, it, ot, causal);
   pl->launch = f;
   // workgroup size of the kernel the pipeline launches (the three-group kernel: int8, HD 128, no causal mask)
-  pl->threads = (groups == 3 && qk8 && hd == 128 && !causal && !dump) ? NW3 * 64 : NW * 64;
+  pl->threads = (groups == 3 && qk8 && hd == 128 && !causal) ? NW3 * 64 : NW * 64;
   pl->ival[0] = split != 0;
   pl->ival[1] = groups == 3;
   return true;

@@ -61,12 +61,13 @@ def attention(gpu: Gpu, q: Tensor, k: Tensor, v: Tensor, out: Tensor, *, Lq: int
 
 def attention_scores(gpu: Gpu, q: Tensor, k: Tensor, v: Tensor, scores: Tensor, *, Lq: int, L: int, H: int,
                      KVH: int, D: int, q_rows: int, k_rows: int, q_scale: Tensor | None = None,
-                     k_scale: Tensor | None = None):
+                     k_scale: Tensor | None = None, **variant):
     """Test hook (no reference counterpart): the raw score accumulators of attention's own MFMA path,
-    scores[h][i][j] = q_i . k_j (int32 for int8 inputs, f32 otherwise), for keys j < L."""
+    scores[h][i][j] = q_i . k_j (int32 for int8 inputs, f32 otherwise), for keys j < L. With int8 inputs at
+    D=128 they come from the kernel that ops.attention would run (GROUPS=2 selects the two-group one)."""
     q8 = q_scale is not None
     vt = v.dtype if v.dtype in ("f16", "bf16") else "bf16"
-    kern = gpu.kernel("attention", "attention_scores", HD=D, QK8=int(q8), IN_T=OUT_DT[vt])
+    kern = gpu.kernel("attention", "attention_scores", HD=D, QK8=int(q8), IN_T=OUT_DT[vt], **variant)
     params = pack("7if3i", Lq, L, H, KVH, q_rows, k_rows, H * D, 1.0, 0, H, 0)
     gpu.launch(kern, None, None, [q, k, v, scores, None, q_scale, k_scale], params, params_index=4)
 

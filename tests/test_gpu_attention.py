@@ -58,9 +58,12 @@ def run_attention(gpu, q, k, v, *, dtype, Lq, L, H, KVH, D, scale, causal=False,
 
 # -- int32 / fp32 score accumulators -------------------------------------------------------------------------------
 
+@pytest.mark.parametrize("groups", [3, 2])
 @pytest.mark.parametrize("Lq,L,H,KVH,D", [(100, 100, 2, 2, 128), (77, 300, 3, 3, 128), (64, 64, 4, 1, 64),
-                                          (300, 1037, 2, 1, 128), (1, 5, 1, 1, 128)])
-def test_int32_scores_bit_exact(gpu, Lq, L, H, KVH, D):
+                                          (300, 1037, 2, 1, 128), (1, 5, 1, 1, 128), (700, 449, 2, 2, 128)])
+def test_int32_scores_bit_exact(gpu, Lq, L, H, KVH, D, groups):
+    """int32 score accumulators of the kernel that runs (int8, D=128: the three-group kernel, or the two-group
+    one with GROUPS=2) equal the exact integer products."""
     rng = np.random.default_rng(Lq + L)
     qi = rng.integers(-127, 128, (H, Lq, D)).astype(np.int8)
     ki = rng.integers(-127, 128, (KVH, L, D)).astype(np.int8)
@@ -71,8 +74,9 @@ def test_int32_scores_bit_exact(gpu, Lq, L, H, KVH, D):
     V = gpu.empty((KVH, k_rows, D), "bf16")
     qs, ks = gpu.upload(np.ones((H, q_rows), np.float32)), gpu.upload(np.ones((KVH, k_rows), np.float32))
     S = gpu.empty((H, Lq, L), "i32")
+    print(f"[scores] groups={groups} Lq={Lq} L={L} H={H} KVH={KVH} D={D}", flush=True)
     ops.attention_scores(gpu, Q, K, V, S, Lq=Lq, L=L, H=H, KVH=KVH, D=D, q_rows=q_rows, k_rows=k_rows,
-                         q_scale=qs, k_scale=ks)
+                         q_scale=qs, k_scale=ks, GROUPS=groups)
     gpu.wait()
     want = oa.int_scores(qi, ki, H_per_kv=H // KVH)
     got = S.numpy()
