@@ -608,7 +608,8 @@ struct Cfg3 {
   static constexpr int NT = NW3 * 64, BQ = NW3 * 32;
   static constexpr int KBYTES = BK * RB, VBYTES = BK * D * 2;
   static constexpr int KOFF = 0, VOFF = 3 * KBYTES, SOFF = VOFF + 3 * VBYTES;
-  static constexpr int LDS = SOFF + 4 * BK * 4;
+  static constexpr int QOFF = SOFF + 4 * BK * 4;  // each wave's Q operand: 4 chunks x 64 lanes x 16 bytes
+  static constexpr int LDS = QOFF + NW3 * 4096;
 };
 
 // DUMP: instead of attention, write this kernel's raw int32 score accumulators S[h][q][key], for tests.
@@ -644,13 +645,15 @@ __global__ __launch_bounds__(NW3 * 64) void attention3_kernel(const char *__rest
   const int q = qb * C::BQ + w * 32 + l32;
   const bool qvalid = q < p.Lq;
 
-  i32x4 qreg[C::NCH];
+  // the Q operand lives in LDS (this wave's own 4 KB), read back for each block's score MFMAs: its 16
+  // registers go to a deeper V operand prefetch
+  char *qlds = smem + C::QOFF + w * 4096 + lane * 16;
   {
     const char *qrow = Q + ((size_t)h * p.q_rows + (qvalid ? q : 0)) * C::RB;
 #pragma unroll
     for (int c = 0; c < C::NCH; c++) {
       const i32x4 v = *(const i32x4 *)(qrow + (2 * c + hl) * 16);
-      qreg[c] = qvalid ? v : i32x4{0, 0, 0, 0};
+      *(i32x4 *)(qlds + c * 1024) = qvalid ? v : i32x4{0, 0, 0, 0};
     }
   }
   const float qsc = qvalid ? fmaxf(qs[(size_t)h * p.q_rows + q] * p.scale, FLT_MIN) : 1.0f;
@@ -758,13 +761,16 @@ __global__ __launch_bounds__(NW3 * 64) void attention3_kernel(const char *__rest
 #pragma unroll
       for (int st = 0; st < 4; st++) {
         if (st < 3) vload(st + 1, va[(st + 1) & 1]);
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int db = 0; db < D / 32; db++) o[db] = mma_pv<VT>(va[st & 1][db], pb[st >> 1][st & 1], o[db]);
       }
     }
     if (j < nblk) {
       const char *Ks = smem + C::KOFF + (j % 3) * C::KBYTES;
-      i32x4 ka[2][C::NCH];
+      i32x4 ka[2][C::NCH], qreg[C::NCH];
+#pragma unroll
+      for (int c = 0; c < C::NCH; c++) qreg[c] = *(const i32x4 *)(qlds + c * 1024);
 #pragma unroll
       for (int t = 0; t < 2; t++)
 #pragma unroll
