@@ -775,6 +775,9 @@ __global__ __launch_bounds__(NW3 * 64) void attention3_kernel(const char *__rest
       for (int t = 0; t < 2; t++)
 #pragma unroll
         for (int c = 0; c < C::NCH; c++) ka[t][c] = *(const i32x4 *)(Ks + kb4[c] + 32 * t * C::RB);
+      // all 12 reads before the first score MFMA (the P V operands' registers are free by now; the scheduler
+      // would otherwise sink each read to its MFMA and expose its latency 8 times)
+      __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
       for (int t = 0; t < 2; t++)
 #pragma unroll
