@@ -40,10 +40,19 @@ CONFIGS = {
 }
 
 
+def to_bf16(x: np.ndarray) -> np.ndarray:
+    """float32 -> bf16 bit patterns (uint16), rounded to nearest even; the synthetic inputs are finite."""
+    b = np.ascontiguousarray(x, dtype=np.float32).view(np.uint32)
+    return ((b + np.uint32(0x7FFF) + ((b >> np.uint32(16)) & np.uint32(1))) >> np.uint32(16)).astype(np.uint16)
+
+
+def from_bf16(b: np.ndarray) -> np.ndarray:
+    return (b.astype(np.uint32) << np.uint32(16)).view(np.float32)
+
+
 def make_inputs(gpu, cfg, rng):
     """Device-resident inputs of one config. Returns (kwargs for ops.attention, prepass closure or None, L)."""
     from h3metal_amd import ops
-    from oracle.bf16 import to_bf16  # bf16 rounding of the synthetic host data only
     H, D, S, L, path = CONFIGS[cfg]
     if L is None:  # config 3: 4096 image rows, text padded to 512 with L_txt ~ U[32, 512] valid
         L = 4096 + int(rng.integers(32, 513))
@@ -77,16 +86,31 @@ def make_inputs(gpu, cfg, rng):
     return dict(q=Q, k=K, v=V), None, L
 
 
-def cpu_baseline(cfg, L, budget_s=20.0):
-    """The oracle's float32 numpy attention (query-chunked) of one head at the config's full size, timed on this
-    host, extrapolated linearly in H to the whole call. Heads are timed until ~budget_s seconds are spent."""
+def head_inputs(kw, cfg, h, L):
+    """Head h of the run's own device inputs as float32 host arrays: the int8 Q/K codes times their scales
+    (what the GPU's scores dequantise to) or the bf16 Q/K, and the bf16 V."""
+    H, D, S, _, _ = CONFIGS[cfg]
+
+    def rows(t, n):
+        return t.view((n, D), offset_elems=h * S * D).numpy()
+    if "q_scale" in kw:
+        q = rows(kw["q"], S).astype(np.float32) * kw["q_scale"].view((S,), offset_elems=h * S).numpy()[:, None]
+        k = rows(kw["k"], L).astype(np.float32) * kw["k_scale"].view((L,), offset_elems=h * S).numpy()[:, None]
+    else:
+        q, k = from_bf16(rows(kw["q"], S)), from_bf16(rows(kw["k"], L))
+    return q, k, from_bf16(rows(kw["v"], L))
+
+
+def cpu_baseline(kw, cfg, L, budget_s=20.0):
+    """The oracle's float32 numpy attention (query-chunked) on this run's own inputs, one head at a time at the
+    config's full size, timed on this host and extrapolated linearly in H to the whole call. Heads are timed
+    until ~budget_s seconds are spent."""
     from oracle.attention import attention_f32_chunked
     H, D, S, _, _ = CONFIGS[cfg]
-    rng = np.random.default_rng(7)
-    q, k, v = (rng.standard_normal((n, D), dtype=np.float32) for n in (S, L, L))
     times = []
     t_start = time.perf_counter()
     while len(times) < H and (not times or time.perf_counter() - t_start < budget_s):
+        q, k, v = head_inputs(kw, cfg, len(times), L)
         t0 = time.perf_counter()
         attention_f32_chunked(q, k, v, D ** -0.5, chunk=512)
         times.append(time.perf_counter() - t0)
@@ -100,8 +124,10 @@ def cpu_baseline(cfg, L, budget_s=20.0):
     except Exception:  # noqa: BLE001
         pass
     return {"value": round(4.0 * H * S * L * D / total / 1e12, 4), "unit": "TFLOP/s",
-            "cores": threads or os.cpu_count(), "kind": "port",
-            "sample": f"{len(times)} of {H} heads at full size (Sq={S}, Sk={L}, D={D}), float32 numpy "
+            "cores": threads or 1, "host_cpus": os.cpu_count(), "kind": "port",
+            "sample": f"heads 0..{len(times) - 1} of {H} of this run's own inputs "
+                      f"({'dequantised int8 Q/K' if 'q_scale' in kw else 'bf16 Q/K'} + bf16 V as float32) at "
+                      f"full size (Sq={S}, Sk={L}, D={D}), float32 numpy "
                       f"(BLAS sgemm + exp, 512-row query chunks), median head time {per_head:.3f} s, "
                       f"extrapolated x{H} heads = {total:.2f} s per call"}
 
@@ -248,7 +274,7 @@ def main():
                     "frac_int8_peak": round(ops_n / gt / PEAK["int8"], 4)}
     out["gemm_q8"] = gl
     if not args.no_cpu:
-        out["cpu_baseline"] = cpu_baseline(args.config, L, args.cpu_budget)
+        out["cpu_baseline"] = cpu_baseline(kw, args.config, L, args.cpu_budget)
     gpu.close()
     print(json.dumps(out), flush=True)
 

@@ -30,8 +30,12 @@ PER_FILE = {
     "qk_prepass.hip": ["-ffp-contract=off"],
     "rot_q8.hip": ["-ffp-contract=off"],
     "gemm.hip": ["-ffp-contract=off"],
+    # score MFMAs with VGPR results (the softmax reads them), P V accumulators in AGPRs (inline assembly)
+    "attention_wave.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"],
 }
-SOURCES = ["capi.hip", "attention.hip", "qk_prepass.hip", "rot_q8.hip", "gemm.hip"]
+# sources whose inline-assembly MFMAs are checked for hazards in the generated code (isa_check.py)
+ISA_CHECKED = ["attention_wave.hip"]
+SOURCES = ["attention_wave.hip", "attention.hip", "capi.hip", "qk_prepass.hip", "rot_q8.hip", "gemm.hip"]
 
 
 def hipcc() -> str:
@@ -47,6 +51,18 @@ def _compile(src: str) -> str:
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode:
         raise RuntimeError(f"compiling {src} failed:\n{' '.join(cmd)}\n{r.stdout}{r.stderr}")
+    if src in ISA_CHECKED:
+        from .isa_check import scan
+        asm = os.path.join(OUT_DIR, src.replace(".hip", ".s"))
+        cmd = [hipcc(), *COMMON, *PER_FILE.get(src, []), "--cuda-device-only", "-S", os.path.join(CSRC, src),
+               "-o", asm]
+        r = subprocess.run(cmd, capture_output=True, text=True)
+        if r.returncode:
+            raise RuntimeError(f"compiling {src} to assembly failed:\n{' '.join(cmd)}\n{r.stdout}{r.stderr}")
+        with open(asm) as f:
+            bad = scan(f.read(), asm)
+        if bad:
+            raise RuntimeError(f"{src}: MFMA hazards in the generated code:\n" + "\n".join(bad[:20]))
     return obj
 
 

@@ -50,7 +50,7 @@
 //    three-group variant (attention3_kernel below: 12 waves, one in its matrix
 //    phase and two in softmax slots per SIMD at any time, LDS-direct staging);
 //    the macro GROUPS=2 keeps them on the two-group kernel.
-#include "h3hip_internal.h"
+#include "attention_common.h"
 
 #include <algorithm>
 #include <cfloat>
@@ -63,92 +63,8 @@
 namespace h3 {
 namespace {
 
-typedef int i32x4 __attribute__((ext_vector_type(4)));
-typedef int i32x16 __attribute__((ext_vector_type(16)));
-typedef float f32x16 __attribute__((ext_vector_type(16)));
-typedef float f32x4 __attribute__((ext_vector_type(4)));
-typedef short i16x4 __attribute__((ext_vector_type(4)));
-typedef short i16x8 __attribute__((ext_vector_type(8)));
-typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
-typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
-typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
-typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
-typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
-
-enum { T_I8 = 0, T_BF16 = 1, T_F16 = 2, T_F32 = 3 };
-
-constexpr int BK = 64;         // keys per LDS block
 constexpr int NW = 8;          // waves per workgroup (two groups of 4)
 constexpr float SLACK = 8.0f;  // log2 units the running maximum may lag behind a score
-
-template <int T> struct Vec8;
-template <> struct Vec8<T_BF16> { using type = bf16x8; using pair = bf16x2; using elem = __bf16; };
-template <> struct Vec8<T_F16> { using type = f16x8; using pair = f16x2; using elem = _Float16; };
-
-// 32x32 score product with a 16-byte A and B operand per lane.
-template <int QKT>
-__device__ __forceinline__ auto mma_qk(i32x4 a, i32x4 b, typename std::conditional<QKT == T_I8, i32x16, f32x16>::type c) {
-  if constexpr (QKT == T_I8) {
-    return __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b, c, 0, 0, 0);
-  } else if constexpr (QKT == T_BF16) {
-    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c,
-                                                   0, 0, 0);
-  } else {
-    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c, 0,
-                                                  0, 0);
-  }
-}
-
-template <int VT>
-__device__ __forceinline__ f32x16 mma_pv(i16x8 a, typename Vec8<VT>::type b, f32x16 c) {
-  if constexpr (VT == T_BF16) return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a), b, c, 0, 0, 0);
-  else return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a), b, c, 0, 0, 0);
-}
-
-// Sum of a packed pair plus an accumulator (v_dot2_f32_{bf16,f16} with (1, 1)).
-template <int VT>
-__device__ __forceinline__ float sum2(typename Vec8<VT>::pair p, float acc) {
-  if constexpr (VT == T_BF16) return __builtin_amdgcn_fdot2_f32_bf16(p, bf16x2{(__bf16)1.0f, (__bf16)1.0f}, acc, false);
-  else return __builtin_amdgcn_fdot2(p, f16x2{(_Float16)1.0f, (_Float16)1.0f}, acc, false);
-}
-
-__device__ __forceinline__ i16x4 lds_tr16(const char *p) {
-  typedef __attribute__((address_space(3))) i16x4 *LP;
-  return __builtin_amdgcn_ds_read_tr16_b64_v4i16((LP)p);
-}
-
-// LDS on gfx950 serves a 16-byte read 16 lanes at a time from 64 four-byte banks (256 bytes per pass).
-// K rows (RB bytes, NP 16-byte pieces) are read 16 lanes = 16 distinct rows at a time: piece p of row `key`
-// is stored at p ^ ((key / (256 / RB)) % NP), so the 16 rows of a pass occupy distinct (bank half, piece)
-// slots. (For 128-byte rows: 2 rows per 256 bytes and 8 pieces each; for 256-byte rows: 16 pieces.)
-template <int RB, int NP>
-__device__ __forceinline__ int kswz(int key) {
-  return (key / (256 / RB)) % NP;
-}
-
-// Byte offset of 16-byte piece pc of V row `key` (rows of D bf16/f16). A transposing read covers 4 rows x 32
-// bytes per 16-lane group, two groups (channels D0 and D0 + 16) per pass: 32-byte unit u of the row is stored at
-// u ^ 2 ((key % 4) / R), R = rows per 256 bytes, which puts the two groups in disjoint bank halves and the
-// four rows of each group in distinct banks.
-template <int D>
-__device__ __forceinline__ int voff(int key, int pc) {
-  constexpr int R = 256 / (D * 2) > 0 ? 256 / (D * 2) : 1;
-  const int u = (pc >> 1) ^ (2 * ((key & 3) / R));
-  return key * (D * 2) + u * 32 + (pc & 1) * 16;
-}
-
-template <int OT>
-__device__ __forceinline__ void store4(char *dst, float a, float b, float c, float d) {
-  if constexpr (OT == T_F32) {
-    *(f32x4 *)dst = f32x4{a, b, c, d};
-  } else if constexpr (OT == T_BF16) {
-    typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
-    *(bf16x4 *)dst = bf16x4{(__bf16)a, (__bf16)b, (__bf16)c, (__bf16)d};
-  } else {
-    typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
-    *(f16x4 *)dst = f16x4{(_Float16)a, (_Float16)b, (_Float16)c, (_Float16)d};
-  }
-}
 
 template <int D, int QKT>
 struct Cfg {
@@ -177,16 +93,6 @@ struct Cfg {
 constexpr int MAGIC = 0x4B400000;
 constexpr float MAGICF = 12582912.0f;
 
-// Tail split: when the last round of workgroups would leave CUs idle, its tiles (the last tiles in tile order)
-// are cut along the keys into `s` chunks of `cb` key blocks each, one workgroup per chunk. A chunk writes its
-// unnormalised partial state (O, running maximum m, row sum l) to `ws`, row stride DG + 4 floats (O at 0,
-// m at DG, l at DG + 1), and attention_merge combines the chunks of a tile.
-struct Split {
-  int nfull;  // workgroups that run whole tiles (tiles 0 .. nfull-1)
-  int s;      // chunks per split tile (0: no split)
-  int cb;     // key blocks per chunk
-  float *ws;  // partial states: [unit][BQ rows][DG + 4]
-};
 
 // DUMP: instead of attention, write the raw score accumulators S[h][q][key]
 // (int32 for int8 inputs, fp32 otherwise) of the same MFMA path, for tests.
@@ -928,59 +834,20 @@ __global__ __launch_bounds__(NW3 * 64) void attention3_kernel(const char *__rest
 }
 
 
-// Combines the chunks of the split tiles: m* = max_c m_c, w_c = 2^(m_c - m*), O = sum_c w_c O_c / sum_c w_c l_c
-// (the online-softmax merge), written like the attention epilogue. One wave per query row, 4 rows per workgroup.
-template <int DG, int OT, int BQ>
-__global__ __launch_bounds__(256) void attention_merge(const float *__restrict__ ws, char *__restrict__ O, AttnParams p,
-                                                       int nqb, int nfull, int s) {
-  constexpr int PER = (DG + 63) / 64;  // channels per lane
-  const int lane = threadIdx.x & 63;
-  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
-  const int tr = row / BQ, r = row - tr * BQ;
-  const int tile = nfull + tr;
-  const int h = tile / nqb, qb = tile - h * nqb;
-  const int q = qb * BQ + r;
-  if (q >= p.Lq) return;
-  const float *w0 = ws + ((size_t)tr * s * BQ + r) * (DG + 4);
-  const size_t ustride = (size_t)BQ * (DG + 4);
-  float mx = -INFINITY;
-  for (int c = 0; c < s; c++) mx = fmaxf(mx, w0[c * ustride + DG]);
-  float lsum = 0.0f, acc[PER];
-#pragma unroll
-  for (int i = 0; i < PER; i++) acc[i] = 0.0f;
-  for (int c = 0; c < s; c++) {
-    const float *wr = w0 + c * ustride;
-    const float mc = wr[DG];
-    const float wt = mc == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(mc - mx);
-    lsum += wt * wr[DG + 1];
-#pragma unroll
-    for (int i = 0; i < PER; i++) {
-      const int d = lane + 64 * i;
-      if (d < DG) acc[i] += wt * wr[d];
-    }
-  }
-  const float inv = lsum > 0.0f ? 1.0f / lsum : 0.0f;
-  constexpr int OSZ = OT == T_F32 ? 4 : 2;
-  const int seq = h / p.seq_heads;
-  char *orow = O + (((size_t)seq * p.seq_rows + q) * p.o_stride + (size_t)(h - seq * p.seq_heads) * DG) * OSZ;
-#pragma unroll
-  for (int i = 0; i < PER; i++) {
-    const int d = lane + 64 * i;
-    if (d < DG) {
-      const float v = acc[i] * inv;
-      if constexpr (OT == T_F32) *(float *)(orow + d * 4) = v;
-      else if constexpr (OT == T_BF16) *(__bf16 *)(orow + d * 2) = (__bf16)v;
-      else *(_Float16 *)(orow + d * 2) = (_Float16)v;
-    }
-  }
-}
-
 int esize(int t) { return t == T_I8 ? 1 : t == T_F32 ? 4 : 2; }
+
+}  // namespace
+
+// R partly filled tiles of a last round, cut into s <= CUs / R chunks: R * s <= CUs units of BQ rows of
+// (D + 4) floats, at the largest BQ (the three-group kernel's 384 rows) and D = 128.
+size_t attention_workspace_max(int cus) { return (size_t)std::max(cus, 1) * Cfg3::BQ * (128 + 4) * sizeof(float); }
+
+namespace {
 
 // Host side: validation (every access the kernel makes must fall inside the
 // bound buffers) and launch.
 template <int D, int QKT, int VT, int OT, bool CAUSAL, bool DUMP>
-int launch_attention(const Pipeline &pl, hipStream_t stream, const Arg *args, int nargs, const void *params,
+int launch_attention(const Pipeline &pl, const Exec &ex, const Arg *args, int nargs, const void *params,
                      uint32_t params_len, std::string *err) {
   using C = Cfg<D == 96 ? 128 : D, QKT>;  // D: the head dim in memory
   if (params_len != sizeof(AttnParams)) {
@@ -1030,9 +897,17 @@ int launch_attention(const Pipeline &pl, hipStream_t stream, const Arg *args, in
   const uint64_t qx = (uint64_t)(p.H - 1) * p.q_rows + p.Lq, kx = (uint64_t)(p.KVH - 1) * p.k_rows + p.L;
   if (!fits(0, qx * D * es, "q") || !fits(1, kx * D * es, "k") || !fits(2, kx * D * 2, "v")) return -1;
   if (qk8 && (!fits(5, qx * 4, "q_scale") || !fits(6, kx * 4, "k_scale"))) return -1;
+  // the wave-pipelined kernel: D = 128 without a causal mask (unless GROUPS selects an older kernel)
+  constexpr bool CANW = !CAUSAL && D == 128;
+  const bool usew = CANW && pl.ival[2];
   if (DUMP) {
-    if (!fits(3, (uint64_t)p.H * p.Lq * p.L * 4, "scores")) return -1;
-  } else if (p.Lq > 0) {
+    if (nargs < 8 || !args[7].ptr) {
+      *err = "the scores hook needs its scores buffer at index 7";
+      return -1;
+    }
+    if (!fits(7, (uint64_t)p.H * p.Lq * p.L * 4, "scores")) return -1;
+  }
+  if (p.Lq > 0 && (!DUMP || usew)) {
     uint64_t last = 0;
     for (int h = 0; h < p.H; h++) {
       const uint64_t seq = h / p.seq_heads;
@@ -1045,11 +920,21 @@ int launch_attention(const Pipeline &pl, hipStream_t stream, const Arg *args, in
     }
     if (!fits(3, last * esize(OT), "out")) return -1;
   }
+  // wide accesses: Q, K, V rows are read 16 bytes at a time, O rows written 4 elements at a time
+  for (int i : {0, 1, 2})
+    if ((uintptr_t)args[i].ptr % 16) {
+      *err = std::string(i == 0 ? "q" : i == 1 ? "k" : "v") + " must be 16-byte aligned";
+      return -1;
+    }
+  if ((!DUMP || usew) && ((uintptr_t)args[3].ptr % (4 * esize(OT)) || p.o_stride % 4)) {
+    *err = "out must be aligned to 4 elements, and its row stride a multiple of 4 elements";
+    return -1;
+  }
   if (p.Lq == 0) return 0;
   // int8 scores, D = 128, no causal mask: the three-group kernel (unless GROUPS=2)
   constexpr bool CAN3 = QKT == T_I8 && !CAUSAL && D == 128;
-  const bool use3 = CAN3 && pl.ival[1];
-  const int BQ = use3 ? Cfg3::BQ : C::BQ;
+  const bool use3 = !usew && CAN3 && pl.ival[1];
+  const int BQ = usew ? WAVE_BQ : use3 ? Cfg3::BQ : C::BQ;
   const int nqb = (p.Lq + BQ - 1) / BQ;
   const long ntiles = (long)nqb * p.H;
   if (ntiles > 0x7fffffffL / 256) {
@@ -1061,20 +946,26 @@ int launch_attention(const Pipeline &pl, hipStream_t stream, const Arg *args, in
   Split sp{(int)ntiles, 0, 0, nullptr};
   const int cus = pl.ival[0] ? cu_count() : 0;
   const int kblocks = (p.L + BK - 1) / BK;
-  if (!CAUSAL && !DUMP && cus > 0) {
+  if (!CAUSAL && (!DUMP || usew) && cus > 0) {
     const int R = (int)(ntiles % cus);
-    const int smax = R ? std::min(cus / R, kblocks / 2) : 0;
+    // chunks per tile: at most CUs / R, at least 2 key blocks each, and as many as the scratch memory holds
+    const size_t unit_bytes = (size_t)BQ * (D + 4) * sizeof(float);
+    const size_t fit = R ? ex.ws_bytes / (unit_bytes * R) : 0;
+    const int smax = R ? (int)std::min<size_t>(std::min(cus / R, kblocks / 2), fit) : 0;
     if (smax >= 2) {
       const int cb = (kblocks + smax - 1) / smax;
       sp.s = (kblocks + cb - 1) / cb;
       sp.cb = cb;
       sp.nfull = (int)ntiles - R;
-      const size_t bytes = (size_t)R * sp.s * BQ * (D + 4) * sizeof(float);
-      sp.ws = (float *)split_workspace(stream, bytes, "attention", err);
-      if (!sp.ws) return -1;
+      sp.ws = (float *)ex.ws;
     }
   }
   const long ngroups = sp.s ? (long)sp.nfull + (ntiles - sp.nfull) * sp.s : ntiles;
+  // the scores hook of the older kernels writes the scores instead of the output
+  char *out = DUMP && !usew ? args[7].ptr : args[3].ptr;
+  if constexpr (CANW) {
+    if (usew) return launch_attention_wave(QKT, VT, OT, DUMP, ex, args, p, nqb, sp, err);
+  }
   if constexpr (CAN3) {
     if (use3) {
       auto kern3 = attention3_kernel<VT, OT, DUMP>;
@@ -1087,11 +978,11 @@ int launch_attention(const Pipeline &pl, hipStream_t stream, const Arg *args, in
         }
         attr3_set = true;
       }
-      hipLaunchKernelGGL(kern3, dim3((unsigned)ngroups), dim3(Cfg3::NT), Cfg3::LDS, stream, args[0].ptr, args[1].ptr,
-                         args[2].ptr, args[3].ptr, (const float *)args[5].ptr, (const float *)args[6].ptr, p, nqb, sp);
+      hipLaunchKernelGGL(kern3, dim3((unsigned)ngroups), dim3(Cfg3::NT), Cfg3::LDS, ex.stream, args[0].ptr, args[1].ptr,
+                         args[2].ptr, out, (const float *)args[5].ptr, (const float *)args[6].ptr, p, nqb, sp);
       if (sp.s) {
         const int rows = (int)(ntiles - sp.nfull) * Cfg3::BQ;
-        hipLaunchKernelGGL((attention_merge<D, OT, Cfg3::BQ>), dim3((unsigned)(rows / 4)), dim3(256), 0, stream, sp.ws,
+        hipLaunchKernelGGL((attention_merge<D, OT, Cfg3::BQ>), dim3((unsigned)(rows / 4)), dim3(256), 0, ex.stream, sp.ws,
                            args[3].ptr, p, nqb, sp.nfull, sp.s);
       }
       return 0;
@@ -1107,11 +998,11 @@ int launch_attention(const Pipeline &pl, hipStream_t stream, const Arg *args, in
     }
     attr_set = true;
   }
-  hipLaunchKernelGGL(kern, dim3((unsigned)ngroups), dim3(C::NT), C::LDS, stream, args[0].ptr, args[1].ptr,
-                     args[2].ptr, args[3].ptr, (const float *)args[5].ptr, (const float *)args[6].ptr, p, nqb, sp);
+  hipLaunchKernelGGL(kern, dim3((unsigned)ngroups), dim3(C::NT), C::LDS, ex.stream, args[0].ptr, args[1].ptr,
+                     args[2].ptr, out, (const float *)args[5].ptr, (const float *)args[6].ptr, p, nqb, sp);
   if (sp.s) {
     const int rows = (int)(ntiles - sp.nfull) * C::BQ;
-    hipLaunchKernelGGL((attention_merge<D, OT, C::BQ>), dim3((unsigned)(rows / 4)), dim3(256), 0, stream, sp.ws, args[3].ptr,
+    hipLaunchKernelGGL((attention_merge<D, OT, C::BQ>), dim3((unsigned)(rows / 4)), dim3(256), 0, ex.stream, sp.ws, args[3].ptr,
                        p, nqb, sp.nfull, sp.s);
   }
   return 0;
@@ -1125,11 +1016,10 @@ LaunchFn pick_causal(bool causal) {
 
 template <int D, int QKT, int VT, bool DUMP>
 LaunchFn pick_out(int ot, bool causal) {
-  if (DUMP) return pick_causal<D, QKT, VT, T_F32, true>(false);
   switch (ot) {
-    case T_BF16: return pick_causal<D, QKT, VT, T_BF16, false>(causal);
-    case T_F16: return pick_causal<D, QKT, VT, T_F16, false>(causal);
-    default: return pick_causal<D, QKT, VT, T_F32, false>(causal);
+    case T_BF16: return pick_causal<D, QKT, VT, T_BF16, DUMP>(causal);
+    case T_F16: return pick_causal<D, QKT, VT, T_F16, DUMP>(causal);
+    default: return pick_causal<D, QKT, VT, T_F32, DUMP>(causal);
   }
 }
 
@@ -1158,8 +1048,9 @@ int type_of(const std::string &s) {
 // as integers and do not change the gfx950 kernel (its tiles are its own).
 // SPLIT (this build's, default 1): allow the tail split of a partly filled
 // last round of workgroups; SPLIT=0 runs every tile whole. GROUPS (this
-// build's, default 3): int8 scores at HD 128 without a causal mask run on the
-// three-group kernel; GROUPS=2 keeps them on the two-group (ping-pong) one.
+// build's, default 1): HD 128 without a causal mask runs on the wave-pipelined
+// kernel; GROUPS=3 selects the three-group kernel (int8 scores) and GROUPS=2 the
+// two-group (ping-pong) one, which also serves every other case.
 bool make_attention(const std::string &fn, const Macros &m, Pipeline *pl, std::string *err) {
   const bool dump = fn == "attention_scores";
   if (fn != "attention" && !dump) {
@@ -1173,9 +1064,9 @@ bool make_attention(const std::string &fn, const Macros &m, Pipeline *pl, std::s
   for (const char *k : {"WM", "BK", "KPAD", "DB", "PVORDER", "VX", "SLACK", "TG"})
     if (!macro_int(m, k, 0, &dummy, err)) return false;
   int split, groups;
-  if (!macro_int(m, "SPLIT", 1, &split, err) || !macro_int(m, "GROUPS", 3, &groups, err)) return false;
-  if (groups != 2 && groups != 3) {
-    *err = "GROUPS must be 2 or 3";
+  if (!macro_int(m, "SPLIT", 1, &split, err) || !macro_int(m, "GROUPS", 1, &groups, err)) return false;
+  if (groups < 1 || groups > 3) {
+    *err = "GROUPS must be 1, 2 or 3";
     return false;
   }
   for (auto &kv : m) {
@@ -1205,9 +1096,11 @@ bool make_attention(const std::string &fn, const Macros &m, Pipeline *pl, std::s
   else f = dump ? pick_types<64, true>(qkt, it, ot, causal) : pick_types<64, false>(qkt, it, ot, causal);
   pl->launch = f;
   // workgroup size of the kernel the pipeline launches (the three-group kernel: int8, HD 128, no causal mask)
-  pl->threads = (groups == 3 && qk8 && hd == 128 && !causal) ? NW3 * 64 : NW * 64;
+  const bool wave = groups == 1 && hd == 128 && !causal;
+  pl->threads = wave ? WAVE_THREADS : (groups == 3 && qk8 && hd == 128 && !causal) ? NW3 * 64 : NW * 64;
   pl->ival[0] = split != 0;
   pl->ival[1] = groups == 3;
+  pl->ival[2] = wave;
   return true;
 }
 

@@ -1,0 +1,591 @@
+// Flash attention for gfx950, wave-pipelined: the kernel that runs D = 128 attention without a causal mask
+// (the DiT path: int8 or 16-bit scores, 16-bit P V). Semantics as attention.hip's kernels, which follow the
+// reference kernel kernels/attention.metal:70-394 (scores in log2 units, key masking at L, int8 scores scaled
+// by qs_i * ks_j, P rounded to the value type, O divided by the row sum at the end).
+#include "attention_common.h"
+
+#include <algorithm>
+
+namespace h3 {
+namespace {
+// ---------------------------------------------------------------------------------------------------------------
+// Wave-pipelined kernel (D = 128, no causal mask; int8 or 16-bit scores): 4 waves per workgroup, one per SIMD
+// (the workgroup's LDS keeps a second one off the CU), 64 query rows per wave (two 32-query MFMA tiles that
+// share every K and V operand read), 256 per workgroup. A single wave overlaps its own MFMAs with its own
+// independent VALU work almost completely on CDNA4 (measured: 4 MFMAs of 32 cycles beside 32 fp32 VALU
+// instructions take the VALU time plus ~5 cycles per MFMA), so the softmax of key block j runs interleaved
+// with the MFMAs of two other blocks, sub-tile by sub-tile: for key tile t (32 keys) and query tile u,
+//     P V of block j-1 (8 MFMAs) | softmax of block j (16 scores per lane) | S of block j+1 (4 to 8 MFMAs)
+// Each sub-tile's score registers are overwritten by block j+1 right after block j's softmax read them, and
+// its P registers by block j right after block j-1's P V read them, so no register set is double-buffered.
+// The running maximum is checked after the exponentials: a block whose per-lane row sum exceeds 2^16 (some
+// score more than ~11 log2 units above the reference maximum; also inf or NaN) or that meets the first valid
+// keys is recomputed in a rare branch from its K and scales (still in their LDS ring slots) with the exact
+// block maximum, after O and l are rescaled. P is bf16 (fp32's exponent range), so a reference up to 2^16 below
+// the true maximum loses no precision.
+// Staging: LDS-direct buffer loads two blocks ahead into 4-deep rings; one barrier per key block.
+// P V MFMA with the O accumulator in AGPRs. Written as assembly so that only O (and Q, an operand the score
+// MFMAs read from AGPRs) lives in the accumulation registers: the score MFMAs are built with VGPR results
+// (-amdgpu-mfma-vgpr-form) and feed the softmax's VALU directly, and the compiler keeps track of their hazards.
+// Hazards it cannot see across this assembly: a VALU read or write of O after these MFMAs is preceded by
+// o_fence(o), and the P operand (written by VALU) is always produced in an earlier key step, behind a barrier.
+// The build checks the generated code for both (h3metal_amd/isa_check.py).
+template <int VT>
+__device__ __forceinline__ void mma_pv_acc(f32x16 &acc, i16x8 a, typename Vec8<VT>::type b) {
+  if constexpr (VT == T_BF16) asm volatile("v_mfma_f32_32x32x16_bf16 %0, %1, %2, %0" : "+a"(acc) : "v"(a), "v"(b));
+  else asm volatile("v_mfma_f32_32x32x16_f16 %0, %1, %2, %0" : "+a"(acc) : "v"(a), "v"(b));
+}
+// Wait states between the last P V MFMA writing O and VALU access to O (a 16-pass XDL result needs 18). The
+// accumulators are operands of the fence, so no access to them can be moved above it.
+__device__ __forceinline__ void o_fence(f32x16 (&o)[2][4]) {
+  asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 4"
+               : "+a"(o[0][0]), "+a"(o[0][1]), "+a"(o[0][2]), "+a"(o[0][3]), "+a"(o[1][0]), "+a"(o[1][1]),
+                 "+a"(o[1][2]), "+a"(o[1][3]));
+}
+
+constexpr int NWV = 4;              // waves per workgroup
+constexpr int BQV = WAVE_BQ;        // query rows per workgroup (64 per wave)
+static_assert(BQV == NWV * 64, "64 query rows per wave");
+constexpr int NRV = 4;              // ring depth (blocks)
+constexpr float SUM_LIMIT = 65536.0f;
+
+template <int QKT>
+struct CfgW {
+  static constexpr bool QK8 = QKT == T_I8;
+  static constexpr int D = 128;
+  static constexpr int ESZ = QK8 ? 1 : 2;
+  static constexpr int RB = D * ESZ;   // bytes per K row
+  static constexpr int NP = RB / 16;   // 16-byte pieces per K row
+  static constexpr int NCH = NP / 2;   // score MFMAs per 32x32 tile
+  static constexpr int KBYTES = BK * RB, VBYTES = BK * D * 2;
+  static constexpr int KOFF = 0, VOFF = NRV * KBYTES, SOFF = VOFF + NRV * VBYTES;
+  static constexpr int LDS = SOFF + (QK8 ? NRV * BK * 4 : 0);
+  static constexpr int KDMA = KBYTES / (NWV * 1024);  // 16-byte LDS-direct loads per wave and block
+  static constexpr int VDMA = VBYTES / (NWV * 1024);
+};
+
+template <int QKT, int VT, int OT, bool DUMP>
+__global__ __launch_bounds__(NWV * 64) __attribute__((amdgpu_waves_per_eu(1, 1)))
+void attention_wave_kernel(const char *__restrict__ Q, const char *__restrict__ K, const char *__restrict__ V,
+                           char *__restrict__ O, const float *__restrict__ qs, const float *__restrict__ ks,
+                           int *__restrict__ dump, AttnParams p, int nqb, Split sp) {
+  using C = CfgW<QKT>;
+  constexpr int D = C::D;
+  constexpr bool QK8 = C::QK8;
+  using VT8 = typename Vec8<VT>::type;
+  using VE = typename Vec8<VT>::elem;
+  using VP2 = typename Vec8<VT>::pair;
+  using SAcc = typename std::conditional<QK8, i32x16, f32x16>::type;
+  extern __shared__ __attribute__((aligned(16))) char smem[];
+  const unsigned lds0 = (unsigned)(size_t)(__attribute__((address_space(3))) char *)smem;
+
+  const int tid = threadIdx.x, lane = tid & 63, hl = lane >> 5, l32 = lane & 31;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int b = blockIdx.x;
+  int lid, unit = -1;
+  if (b < sp.nfull) {
+    const int nb = sp.nfull;
+    const int per = nb >> 3, rem = nb & 7, xcd = b & 7, loc = b >> 3;
+    lid = (xcd < rem ? xcd * (per + 1) : rem * (per + 1) + (xcd - rem) * per) + loc;
+  } else {
+    unit = b - sp.nfull;
+    lid = sp.nfull + unit / sp.s;
+  }
+  const int h = lid / nqb, qb = lid - h * nqb;
+  const int kvh = h / (p.H / p.KVH);
+  // this lane's query rows: q0 + 32 u for the two query tiles u
+  const int q0 = qb * BQV + w * 64 + l32;
+
+  // Q operands (B of S^T = K Q^T), kept in registers: row q0 + 32 u, piece 2c + hl of each 32-byte chunk c
+  i32x4 qreg[2][C::NCH];
+#pragma unroll
+  for (int u = 0; u < 2; u++) {
+    const int q = q0 + 32 * u;
+    const bool ok = q < p.Lq;
+    const char *qrow = Q + ((size_t)h * p.q_rows + (ok ? q : 0)) * C::RB;
+#pragma unroll
+    for (int c = 0; c < C::NCH; c++) {
+      i32x4 v = *(const i32x4 *)(qrow + (2 * c + hl) * 16);
+      qreg[u][c] = ok ? v : i32x4{0, 0, 0, 0};
+      asm volatile("" : "+a"(qreg[u][c]));  // from here on Q lives in AGPRs only
+    }
+  }
+  float qsc[2];
+#pragma unroll
+  for (int u = 0; u < 2; u++) {
+    const int q = q0 + 32 * u;
+    qsc[u] = p.scale;
+    if constexpr (QK8) qsc[u] = q < p.Lq ? fmaxf(qs[(size_t)h * p.q_rows + q] * p.scale, FLT_MIN) : 1.0f;
+  }
+
+  int key0 = 0, Lk = p.L;
+  if (unit >= 0) {
+    key0 = (unit % sp.s) * sp.cb * BK;
+    Lk = min(p.L, key0 + sp.cb * BK) - key0;
+  }
+  const char *Kh = K + ((size_t)kvh * p.k_rows + key0) * C::RB;
+  const char *Vh = V + ((size_t)kvh * p.k_rows + key0) * D * 2;
+  const float *ksh = QK8 ? ks + (size_t)kvh * p.k_rows + key0 : nullptr;
+  const int nblk = Lk > 0 ? (Lk + BK - 1) / BK : 0;
+
+  // -- LDS-direct staging. Load instruction r of this wave writes 1 KB at LDS (r * NWV + w) * 1024 of the block's
+  // ring slot; each lane fetches the 16-byte piece whose swizzled position that is. Rows at or past Lk read as
+  // zero (descriptor range).
+  auto rsrc = [&](const void *base, int blk, int row_bytes) {
+    const int rows = max(0, Lk - blk * BK);
+    return __builtin_amdgcn_make_buffer_rsrc((void *)((const char *)base + (size_t)blk * BK * row_bytes), (short)0,
+                                             __builtin_amdgcn_readfirstlane(rows * row_bytes), 0x00020000);
+  };
+  unsigned kgo[C::KDMA], vgo[C::VDMA];
+#pragma unroll
+  for (int r = 0; r < C::KDMA; r++) {
+    const int o = (r * NWV + w) * 1024 + 16 * lane;
+    const int row = o / C::RB, slot = (o / 16) % C::NP;
+    kgo[r] = row * C::RB + (slot ^ kswz<C::RB, C::NP>(row)) * 16;
+  }
+#pragma unroll
+  for (int r = 0; r < C::VDMA; r++) {
+    const int o = (r * NWV + w) * 1024 + 16 * lane;
+    const int row = o >> 8, uu = (o & 255) >> 5, sub = (o >> 4) & 1;
+    vgo[r] = row * (D * 2) + (2 * (uu ^ (2 * (row & 3))) + sub) * 16;
+  }
+  auto stage_k = [&](int blk) {  // K and key scales of block blk
+    const int slot = blk % NRV;
+    const __amdgpu_buffer_rsrc_t rk = rsrc(Kh, blk, C::RB);
+#pragma unroll
+    for (int r = 0; r < C::KDMA; r++) dma16(lds0 + C::KOFF + slot * C::KBYTES + (r * NWV + w) * 1024, kgo[r], rk);
+    // every wave loads the block's 64 scales to the same place (no wave-dependent branch or wait count)
+    if constexpr (QK8) dma4(lds0 + C::SOFF + slot * BK * 4, lane * 4, rsrc(ksh, blk, 4));
+  };
+  auto stage_v = [&](int blk) {
+    const __amdgpu_buffer_rsrc_t rv = rsrc(Vh, blk, D * 2);
+#pragma unroll
+    for (int r = 0; r < C::VDMA; r++)
+      dma16(lds0 + C::VOFF + (blk % NRV) * C::VBYTES + (r * NWV + w) * 1024, vgo[r], rv);
+  };
+
+  f32x16 o[2][D / 32];
+#pragma unroll
+  for (int u = 0; u < 2; u++)
+#pragma unroll
+    for (int db = 0; db < D / 32; db++)
+#pragma unroll
+      for (int i = 0; i < 16; i++) o[u][db][i] = 0.0f;
+  float m[2] = {-INFINITY, -INFINITY}, l[2] = {0.0f, 0.0f};
+  SAcc s[2][2];    // [key tile t][query tile u]
+  VT8 pb[2][2][2]; // [t][u][16-key step within t]
+#pragma unroll
+  for (int t = 0; t < 2; t++)
+#pragma unroll
+    for (int u = 0; u < 2; u++) {
+#pragma unroll
+      for (int i = 0; i < 16; i++) s[t][u][i] = 0;
+#pragma unroll
+      for (int i = 0; i < 16; i++) pb[t][u][i >> 3][i & 7] = (VE)0.0f;
+    }
+
+  const int krow = 16 * (l32 >> 4) + 8 * ((l32 >> 2) & 1) + 4 * ((l32 >> 3) & 1) + (l32 & 3);
+  const int l16 = lane & 15;
+  const int tr_row = l16 >> 2, tr_col = (l16 & 3) * 8;
+  unsigned vbase[D / 32], kbase[C::NCH];
+  {
+    const int k0 = 8 * hl + tr_row;
+#pragma unroll
+    for (int db = 0; db < D / 32; db++) vbase[db] = voff<D>(k0, (db * 32 + (l32 & 16)) / 8) + tr_col;
+#pragma unroll
+    for (int c = 0; c < C::NCH; c++) kbase[c] = krow * C::RB + (((2 * c + hl) ^ kswz<C::RB, C::NP>(krow)) * 16);
+  }
+
+  // K operands of key tile t of block j (A of S^T = K Q^T)
+  auto kops = [&](int j, int t, i32x4 (&ka)[C::NCH]) {
+    const char *Ks = smem + C::KOFF + (j % NRV) * C::KBYTES + 32 * t * C::RB;
+#pragma unroll
+    for (int c = 0; c < C::NCH; c++) ka[c] = *(const i32x4 *)(Ks + kbase[c]);
+  };
+  auto score_mfmas = [&](SAcc &acc, const i32x4 (&ka)[C::NCH], int u) {
+#pragma unroll
+    for (int c = 0; c < C::NCH; c++) acc = mma_qk<QKT>(ka[c], qreg[u][c], c == 0 ? SAcc{} : acc);
+  };
+  // V operands of key tile t of block j: [16-key step][channel block]
+  auto vops = [&](int j, int t, i16x8 (&va)[2][D / 32]) {
+    const char *Vs = smem + C::VOFF + (j % NRV) * C::VBYTES;
+#pragma unroll
+    for (int s2 = 0; s2 < 2; s2++) {
+      const int koff = (32 * t + 16 * s2) * (D * 2);
+#pragma unroll
+      for (int db = 0; db < D / 32; db++) {
+        const i16x4 lo = lds_tr16(Vs + vbase[db] + koff);
+        const i16x4 hi = lds_tr16(Vs + vbase[db] + koff + 4 * (D * 2));
+        va[s2][db] = i16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+      }
+    }
+  };
+  // key scales of key tile t of block j, for this lane's 16 keys
+  auto kscales = [&](int j, int t, f32x4 (&k4)[2][2]) {
+    const float *ksc = (const float *)(smem + C::SOFF) + (j % NRV) * BK;
+#pragma unroll
+    for (int s8 = 0; s8 < 2; s8++)
+#pragma unroll
+      for (int hh = 0; hh < 2; hh++) k4[s8][hh] = *(const f32x4 *)(ksc + 32 * t + 16 * s8 + 8 * hl + 4 * hh);
+  };
+  // scores of sub-tile (t, u) of block j in log2 units before the query scale; keys >= Lk at -inf (MASK)
+  auto to_x = [&](const SAcc &acc, const f32x4 (&k4)[2][2], int j, int t, bool mask) {
+    f32x16 x;
+    if constexpr (QK8) {
+#pragma unroll
+      for (int s8 = 0; s8 < 2; s8++)
+#pragma unroll
+        for (int hh = 0; hh < 2; hh++)
+#pragma unroll
+          for (int e = 0; e < 4; e++) {
+            const int i = 8 * s8 + 4 * hh + e;
+            x[i] = (float)acc[i] * k4[s8][hh][e];
+          }
+    } else {
+      x = acc;
+    }
+    if (mask) {
+#pragma unroll
+      for (int i = 0; i < 16; i++)
+        if (j * BK + 32 * t + 16 * (i >> 3) + 8 * hl + (i & 7) >= Lk) x[i] = -INFINITY;
+    }
+    return x;
+  };
+  auto exps = [&](const f32x16 &x, float qs_u, float nm, VT8 (&pr)[2]) {
+    float acc0 = 0.0f, acc1 = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 16; i += 2) {
+      const float p0 = __builtin_amdgcn_exp2f(fmaf(x[i], qs_u, nm));
+      const float p1 = __builtin_amdgcn_exp2f(fmaf(x[i + 1], qs_u, nm));
+      const VP2 pp = {(VE)p0, (VE)p1};
+      pr[i >> 3][i & 7] = pp[0];
+      pr[i >> 3][(i & 7) + 1] = pp[1];
+      if (i & 2) acc1 = sum2<VT>(pp, acc1);
+      else acc0 = sum2<VT>(pp, acc0);
+    }
+    return acc0 + acc1;
+  };
+  auto dump_scores = [&](const SAcc &acc, int j, int t, int u) {
+    if constexpr (DUMP) {
+      const int q = q0 + 32 * u;
+      if (q < p.Lq) {
+        // four consecutive keys at a time, taken out of the accumulator as vectors (element-wise extraction of
+        // an MFMA result vector has been miscompiled into a splat of element 0)
+        const i32x16 a = __builtin_bit_cast(i32x16, acc);
+        const i32x4 g[4] = {__builtin_shufflevector(a, a, 0, 1, 2, 3), __builtin_shufflevector(a, a, 4, 5, 6, 7),
+                            __builtin_shufflevector(a, a, 8, 9, 10, 11), __builtin_shufflevector(a, a, 12, 13, 14, 15)};
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+          const int key = key0 + j * BK + 32 * t + 16 * (r >> 1) + 8 * hl + 4 * (r & 1);
+          int *dst = dump + ((size_t)h * p.Lq + q) * p.L + key;
+          if (key + 4 <= key0 + Lk && (p.L & 3) == 0) {
+            *(i32x4 *)dst = g[r];
+          } else {
+#pragma unroll
+            for (int e = 0; e < 4; e++)
+              if (key + e < key0 + Lk) dst[e] = g[r][e];
+          }
+        }
+      }
+    }
+  };
+
+  // Operands of one key tile (32 keys) of a step: V of block j - 1 (A of the P V MFMAs: [16-key step][channel
+  // block]), K of block j + 1 (A of the score MFMAs) and the key scales of block j.
+  struct Ops {
+    i16x8 va[8];  // index 4 * s2 + db
+    i32x4 ka[C::NCH];
+    f32x4 k4[4];  // keys 32 t + 16 (g / 2) + 8 hl + 4 (g % 2) + e of score group g
+  };
+  auto vread = [&](int j, int t, int k) {  // V(j) operand k of key tile t
+    const char *Vs = smem + C::VOFF + (j % NRV) * C::VBYTES + (32 * t + 16 * (k >> 2)) * (D * 2) + vbase[k & 3];
+    const i16x4 lo = lds_tr16(Vs);
+    const i16x4 hi = lds_tr16(Vs + 4 * (D * 2));
+    return i16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+  };
+  auto kread = [&](int j, int t, int c) {  // K(j) operand, chunk c of key tile t
+    return *(const i32x4 *)(smem + C::KOFF + (j % NRV) * C::KBYTES + 32 * t * C::RB + kbase[c]);
+  };
+  auto sread = [&](int j, int t, int g) {  // scales of K(j), score group g of key tile t
+    return *(const f32x4 *)((const float *)(smem + C::SOFF) + (j % NRV) * BK + 32 * t + 16 * (g >> 1) + 8 * hl +
+                            4 * (g & 1));
+  };
+  auto load_ops = [&](Ops &op, int j, int t) {  // all operands of tile t of step j
+#pragma unroll
+    for (int g = 0; g < 4; g++)
+      if constexpr (QK8) op.k4[g] = sread(j, t, g);
+#pragma unroll
+    for (int k = 0; k < 8; k++) op.va[k] = vread(j - 1, t, k);
+#pragma unroll
+    for (int c = 0; c < C::NCH; c++) op.ka[c] = kread(j + 1, t, c);
+  };
+
+  // One (key tile t, query tile u) sub-tile of step j, in issue order: the P V MFMAs of block j - 1 and the
+  // score MFMAs of block j + 1 spread between short runs of independent VALU work (groups of 4 scores of block j
+  // in flight at once; the matrix pipe accepts one MFMA per 32 cycles, and a lone wave stalls on back-to-back
+  // MFMAs and on VALU results it needs too early). When `refresh`, each operand is replaced by the one of the
+  // next tile (jn, tn) right after its last use here.
+  auto sub_tile = [&](Ops &op, int j, int t, int u, bool has_pv, bool has_next, bool mask, bool refresh, int jn,
+                      int tn, float &bsum) {
+    dump_scores(s[t][u], j, t, u);
+    const float nm = m[u] == -INFINITY ? 0.0f : -m[u];
+    float xv[16];
+    float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    int npv = 0, ns = 0;
+    auto pv = [&]() {  // next P V MFMA of this sub-tile (the operand refresh also when there is none)
+      const int k = npv++;
+      if (has_pv) mma_pv_acc<VT>(o[u][k & 3], op.va[k], pb[t][u][k >> 2]);
+      if (refresh) op.va[k] = vread(jn - 1, tn, k);
+    };
+    auto sm = [&]() {  // next score MFMA of this sub-tile
+      const int c = ns++;
+      if (has_next) s[t][u] = mma_qk<QKT>(op.ka[c], qreg[u][c], c == 0 ? SAcc{} : s[t][u]);
+      if (refresh) op.ka[c] = kread(jn + 1, tn, c);
+    };
+    // VALU stages on score group g (scores 4 g .. 4 g + 3)
+    auto cv = [&](int g) {  // int8: int32 -> float; 16-bit: the fp32 score itself
+#pragma unroll
+      for (int e = 0; e < 4; e++) {
+        const int i = 4 * g + e;
+        if constexpr (QK8) xv[i] = (float)s[t][u][i];
+        else xv[i] = s[t][u][i];
+      }
+    };
+    auto mu = [&](int g) {  // times the key scale (int8); keys past Lk to -inf
+#pragma unroll
+      for (int e = 0; e < 4; e++) {
+        const int i = 4 * g + e;
+        if constexpr (QK8) xv[i] *= op.k4[g][e];
+        if (mask && j * BK + 32 * t + 16 * (i >> 3) + 8 * hl + (i & 7) >= Lk) xv[i] = -INFINITY;
+      }
+      if (QK8 && refresh && u == 1) op.k4[g] = sread(jn, tn, g);
+    };
+    auto fm = [&](int g) {
+#pragma unroll
+      for (int e = 0; e < 4; e++) xv[4 * g + e] = fmaf(xv[4 * g + e], qsc[u], nm);
+    };
+    auto ex = [&](int g) {
+#pragma unroll
+      for (int e = 0; e < 4; e++) xv[4 * g + e] = __builtin_amdgcn_exp2f(xv[4 * g + e]);
+    };
+    auto pk = [&](int g) {  // round to the value type, into the P operand, and sum the rounded values
+#pragma unroll
+      for (int e = 0; e < 4; e += 2) {
+        const int i = 4 * g + e;
+        const VP2 pp = {(VE)xv[i], (VE)xv[i + 1]};
+        pb[t][u][i >> 3][i & 7] = pp[0];
+        pb[t][u][i >> 3][(i & 7) + 1] = pp[1];
+        acc[(g & 1) * 2 + (e >> 1)] = sum2<VT>(pp, acc[(g & 1) * 2 + (e >> 1)]);
+      }
+    };
+#define SB __builtin_amdgcn_sched_barrier(0)
+    if constexpr (QK8) {
+      // 8 P V, 4 score MFMAs; 16 scores x (cvt, mul, fma, exp) + 8 (pack, sum)
+      pv(); cv(0); SB; cv(1); SB; pv(); mu(0); SB; cv(2); SB; pv(); mu(1); SB; fm(0); SB; pv(); cv(3); SB;
+      mu(2); SB; pv(); fm(1); SB; ex(0); SB; pv(); mu(3); SB; fm(2); SB; pv(); ex(1); SB; sm(); fm(3); SB;
+      pv(); ex(2); SB; sm(); pk(0); SB; ex(3); SB; sm(); pk(1); SB; pk(2); SB; sm(); pk(3); SB;
+    } else {
+      // 8 P V, 8 score MFMAs; 16 scores x (fma, exp) + 8 (pack, sum); mu() only masks here
+      pv(); cv(0); cv(1); mu(0); mu(1); SB; pv(); fm(0); SB; pv(); fm(1); SB; pv(); cv(2); cv(3); mu(2); mu(3);
+      ex(0); SB; pv(); fm(2); SB;
+      pv(); ex(1); SB; pv(); fm(3); SB; pv(); ex(2); SB; sm(); pk(0); SB; sm(); ex(3); SB; sm(); pk(1); SB;
+      sm(); SB; sm(); pk(2); SB; sm(); SB; sm(); pk(3); SB; sm(); SB;
+    }
+#undef SB
+    bsum += (acc[0] + acc[1]) + (acc[2] + acc[3]);
+  };
+
+  // Step j: P V of block j - 1, softmax of block j, scores of block j + 1. The barrier sits before the last
+  // sub-tile: the loads issued after it (K and scales of block j + 3, V of block j + 1) land during the next
+  // step, and the last sub-tile reads the first operands of the next step, all of which landed and were
+  // published by that barrier. Ring slots (4 deep): K(j + 3) replaces K(j - 1), last read in step j - 1's
+  // recompute; V(j + 1) replaces V(j - 3); scales(j + 3) replace scales(j - 1).
+  auto step = [&](Ops &op, int j, bool has_pv, bool has_next, bool mask) {
+    float bs[2] = {0.0f, 0.0f};
+    sub_tile(op, j, 0, 0, has_pv, has_next, mask, false, 0, 0, bs[0]);
+    sub_tile(op, j, 0, 1, has_pv, has_next, mask, true, j, 1, bs[1]);
+    sub_tile(op, j, 1, 0, has_pv, has_next, mask, false, 0, 0, bs[0]);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this wave's loads of the previous step
+    __syncthreads();
+    stage_k(j + 3);
+    stage_v(j + 1);
+    sub_tile(op, j, 1, 1, has_pv, has_next, mask, true, j + 1, 0, bs[1]);
+    // rare: a score far above the reference maximum, or the first valid keys of a row: recompute block j's
+    // P with the exact maximum
+    bool bad = false;
+#pragma unroll
+    for (int u = 0; u < 2; u++) bad = bad || !(bs[u] <= SUM_LIMIT) || m[u] == -INFINITY;
+    if (__builtin_expect(__any(bad), 0)) {
+      o_fence(o);  // P V MFMAs of this step may still be writing O
+#pragma unroll
+      for (int u = 0; u < 2; u++) {
+        // block j's scores of query tile u again (K and scales are still in their ring slots)
+        f32x16 xs[2];
+        float bmax = -INFINITY;
+#pragma unroll
+        for (int t = 0; t < 2; t++) {
+          i32x4 ka[C::NCH];
+          kops(j, t, ka);
+          f32x4 k4[2][2];
+          if constexpr (QK8) kscales(j, t, k4);
+          SAcc acc;
+          score_mfmas(acc, ka, u);
+          xs[t] = to_x(acc, k4, j, t, mask);
+#pragma unroll
+          for (int i = 0; i < 16; i++) bmax = fmaxf(bmax, xs[t][i]);
+        }
+        const float pm = fmaxf(bmax, __shfl_xor(bmax, 32)) * qsc[u];
+        const float mn = fmaxf(m[u], pm);
+        const float f = (m[u] == -INFINITY || mn == -INFINITY) ? 1.0f : __builtin_amdgcn_exp2f(m[u] - mn);
+        m[u] = mn;
+        l[u] *= f;
+#pragma unroll
+        for (int db = 0; db < D / 32; db++)
+#pragma unroll
+          for (int i = 0; i < 16; i++) o[u][db][i] *= f;
+        const float nm = mn == -INFINITY ? 0.0f : -mn;
+        bs[u] = exps(xs[0], qsc[u], nm, pb[0][u]) + exps(xs[1], qsc[u], nm, pb[1][u]);
+      }
+      asm volatile("s_nop 2" ::: "memory");  // VALU writes of O before the next MFMA reads it
+    }
+    l[0] += bs[0];
+    l[1] += bs[1];
+  };
+
+  if (nblk > 0) {
+    stage_k(0);
+    stage_k(1);
+    stage_k(2);
+    stage_v(0);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    {
+      i32x4 ka[C::NCH];
+#pragma unroll
+      for (int t = 0; t < 2; t++) {
+        kops(0, t, ka);
+#pragma unroll
+        for (int u = 0; u < 2; u++) score_mfmas(s[t][u], ka, u);
+      }
+    }
+    Ops op;
+    load_ops(op, 0, 0);
+    // first block (no P V yet), the steady state (no masking: every key of the block is valid), the last block
+    if (nblk == 1) step(op, 0, false, false, true);
+    else step(op, 0, false, true, false);
+    for (int j = 1; j + 1 < nblk; j++) step(op, j, true, true, false);
+    if (nblk > 1) step(op, nblk - 1, true, false, true);
+    // P V of the last block (its tile-0 V operands were read by the last step)
+#pragma unroll
+    for (int t = 0; t < 2; t++) {
+      if (t == 1) {
+#pragma unroll
+        for (int k = 0; k < 8; k++) op.va[k] = vread(nblk - 1, 1, k);
+      }
+#pragma unroll
+      for (int u = 0; u < 2; u++)
+#pragma unroll
+        for (int k = 0; k < 8; k++) mma_pv_acc<VT>(o[u][k & 3], op.va[k], pb[t][u][k >> 2]);
+    }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // loads past the last block land before the exit
+    o_fence(o);  // inside the branch: no copy of O may come between the last MFMA and the fence
+  }
+
+#pragma unroll
+  for (int u = 0; u < 2; u++) {
+    const int q = q0 + 32 * u;
+    const float lt = l[u] + __shfl_xor(l[u], 32);
+    if (unit >= 0) {
+      float *wrow = sp.ws + ((size_t)unit * BQV + (q - qb * BQV)) * (D + 4);
+#pragma unroll
+      for (int db = 0; db < D / 32; db++)
+#pragma unroll
+        for (int g = 0; g < 4; g++)
+          store4<T_F32>((char *)(wrow + db * 32 + 8 * g + 4 * hl), o[u][db][4 * g], o[u][db][4 * g + 1],
+                        o[u][db][4 * g + 2], o[u][db][4 * g + 3]);
+      if (hl == 0) {
+        wrow[D] = m[u];
+        wrow[D + 1] = lt;
+      }
+      continue;
+    }
+    const float inv = lt > 0.0f ? 1.0f / lt : 0.0f;
+    if (q < p.Lq) {
+      constexpr int OSZ = OT == T_F32 ? 4 : 2;
+      const int seq = h / p.seq_heads;
+      char *orow = O + (((size_t)seq * p.seq_rows + q) * p.o_stride + (size_t)(h - seq * p.seq_heads) * D) * OSZ;
+#pragma unroll
+      for (int db = 0; db < D / 32; db++)
+#pragma unroll
+        for (int g = 0; g < 4; g++) {
+          const int d = db * 32 + 8 * g + 4 * hl;
+          store4<OT>(orow + d * OSZ, o[u][db][4 * g] * inv, o[u][db][4 * g + 1] * inv, o[u][db][4 * g + 2] * inv,
+                     o[u][db][4 * g + 3] * inv);
+        }
+    }
+  }
+}
+
+
+}  // namespace
+
+#ifndef WAVE_KERNEL_ONLY
+int launch_attention_wave(int qkt, int vt, int ot, bool dump, const Exec &ex, const Arg *args, const AttnParams &p,
+                          int nqb, const Split &sp, std::string *err) {
+  auto run = [&](auto kern, int lds) -> int {
+    static bool attr_set[2][4][4][2] = {};  // one per specialisation (qkt, vt, ot, dump)
+    bool &set = attr_set[qkt == T_I8][vt][ot][dump];
+    if (!set) {
+      hipError_t e = hipFuncSetAttribute((const void *)kern, hipFuncAttributeMaxDynamicSharedMemorySize, lds);
+      if (e != hipSuccess) {
+        *err = std::string("hipFuncSetAttribute: ") + hipGetErrorString(e);
+        return -1;
+      }
+      set = true;
+    }
+    const long ntiles = (long)nqb * p.H;
+    const long ngroups = sp.s ? (long)sp.nfull + (ntiles - sp.nfull) * sp.s : ntiles;
+    hipLaunchKernelGGL(kern, dim3((unsigned)ngroups), dim3(NWV * 64), lds, ex.stream, args[0].ptr, args[1].ptr,
+                       args[2].ptr, args[3].ptr, (const float *)args[5].ptr, (const float *)args[6].ptr,
+                       dump ? (int *)args[7].ptr : nullptr, p, nqb, sp);
+    if (sp.s) {
+      const int rows = (int)(ntiles - sp.nfull) * BQV;
+      switch (ot) {
+        case T_BF16:
+          hipLaunchKernelGGL((attention_merge<128, T_BF16, BQV>), dim3((unsigned)(rows / 4)), dim3(256), 0, ex.stream,
+                             sp.ws, args[3].ptr, p, nqb, sp.nfull, sp.s);
+          break;
+        case T_F16:
+          hipLaunchKernelGGL((attention_merge<128, T_F16, BQV>), dim3((unsigned)(rows / 4)), dim3(256), 0, ex.stream,
+                             sp.ws, args[3].ptr, p, nqb, sp.nfull, sp.s);
+          break;
+        default:
+          hipLaunchKernelGGL((attention_merge<128, T_F32, BQV>), dim3((unsigned)(rows / 4)), dim3(256), 0, ex.stream,
+                             sp.ws, args[3].ptr, p, nqb, sp.nfull, sp.s);
+      }
+    }
+    return 0;
+  };
+  auto with_ot = [&](auto qk_c, auto v_c, auto d_c) -> int {
+    constexpr int QKT = decltype(qk_c)::value, VT = decltype(v_c)::value;
+    constexpr bool DUMP = decltype(d_c)::value;
+    constexpr int LDS = CfgW<QKT>::LDS;
+    switch (ot) {
+      case T_BF16: return run(attention_wave_kernel<QKT, VT, T_BF16, DUMP>, LDS);
+      case T_F16: return run(attention_wave_kernel<QKT, VT, T_F16, DUMP>, LDS);
+      default: return run(attention_wave_kernel<QKT, VT, T_F32, DUMP>, LDS);
+    }
+  };
+  using I8 = std::integral_constant<int, T_I8>;
+  using B16 = std::integral_constant<int, T_BF16>;
+  using F16 = std::integral_constant<int, T_F16>;
+  auto with_dump = [&](auto qk_c, auto v_c) -> int {
+    return dump ? with_ot(qk_c, v_c, std::true_type{}) : with_ot(qk_c, v_c, std::false_type{});
+  };
+  if (qkt == T_I8) return vt == T_BF16 ? with_dump(I8{}, B16{}) : with_dump(I8{}, F16{});
+  if (qkt == T_BF16) return with_dump(B16{}, B16{});
+  return with_dump(F16{}, F16{});
+}
+#endif
+
+}  // namespace h3

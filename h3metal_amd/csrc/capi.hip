@@ -96,30 +96,6 @@ int cu_count() {
   return cache[dev];
 }
 
-// Workspace of the tail splits (attention's partial states, the GEMM's partial products), per stream: work on
-// one stream is ordered, so one buffer per stream is never used by two launches at once; grown on demand and
-// kept until the process ends.
-void *split_workspace(hipStream_t stream, size_t bytes, const char *who, std::string *err) {
-  static std::mutex mu;
-  static std::map<hipStream_t, std::pair<void *, size_t>> bufs;
-  std::lock_guard<std::mutex> lock(mu);
-  auto &e = bufs[stream];
-  if (e.second < bytes) {
-    if (e.first) {
-      hipStreamSynchronize(stream);  // the old buffer may still be read by queued work
-      hipFree(e.first);
-      e = {nullptr, 0};
-    }
-    void *ptr = nullptr;
-    if (hipMalloc(&ptr, bytes) != hipSuccess) {
-      *err = std::string(who) + ": cannot allocate the " + std::to_string(bytes) + "-byte split workspace";
-      return nullptr;
-    }
-    e = {ptr, bytes};
-  }
-  return e.first;
-}
-
 }  // namespace h3
 
 struct h3_ctx {
@@ -128,6 +104,10 @@ struct h3_ctx {
   std::string name;
   uint64_t free_at_open = 0, total = 0;
   std::map<std::string, std::unique_ptr<h3::Pipeline>> pipelines;
+  // scratch memory of the launches on this context's stream (work on one stream is ordered, so one buffer
+  // serves every launch); sized at open for the attention split, grown only by h3_reserve_workspace
+  void *ws = nullptr;
+  size_t ws_bytes = 0;
   // timing of the work since the last wait
   hipEvent_t t0 = nullptr, t1 = nullptr;
   bool timing = false;
@@ -190,18 +170,44 @@ h3_ctx *h3_open(const char *kernel_dir) {
     delete ctx;
     return nullptr;
   }
+  const size_t ws = h3::attention_workspace_max(h3::cu_count());
+  if (!hip_ok(hipMalloc(&ctx->ws, ws), "cannot allocate the dispatch scratch memory")) {
+    h3_close(ctx);
+    return nullptr;
+  }
+  ctx->ws_bytes = ws;
   return ctx;
 }
 
 void h3_close(h3_ctx *ctx) {
   if (!ctx) return;
-  hipStreamSynchronize(ctx->stream);
+  if (ctx->stream) hipStreamSynchronize(ctx->stream);
   drain_profile(ctx);
-  hipEventDestroy(ctx->t0);
-  hipEventDestroy(ctx->t1);
-  hipStreamDestroy(ctx->stream);
+  if (ctx->ws) hipFree(ctx->ws);
+  if (ctx->t0) hipEventDestroy(ctx->t0);
+  if (ctx->t1) hipEventDestroy(ctx->t1);
+  if (ctx->stream) hipStreamDestroy(ctx->stream);
   delete ctx;
 }
+
+int h3_reserve_workspace(h3_ctx *ctx, uint64_t bytes) {
+  if (!ctx) {
+    set_error("h3_reserve_workspace: no context");
+    return -1;
+  }
+  if (bytes <= ctx->ws_bytes) return 0;
+  // queued work may still use the old buffer
+  if (!hip_ok(hipStreamSynchronize(ctx->stream), "hipStreamSynchronize")) return -1;
+  void *p = nullptr;
+  if (!hip_ok(hipMalloc(&p, bytes), ("cannot allocate " + std::to_string(bytes) + " bytes of scratch").c_str()))
+    return -1;
+  hipFree(ctx->ws);
+  ctx->ws = p;
+  ctx->ws_bytes = bytes;
+  return 0;
+}
+
+uint64_t h3_workspace_bytes(h3_ctx *ctx) { return ctx ? ctx->ws_bytes : 0; }
 
 const char *h3_device_name(h3_ctx *ctx) { return ctx ? ctx->name.c_str() : ""; }
 uint64_t h3_recommended_working_set(h3_ctx *ctx) { return ctx ? ctx->free_at_open : 0; }
@@ -359,7 +365,11 @@ int h3_dispatch(h3_ctx *ctx, void *pso, const uint32_t grid[3], const uint32_t t
       return -1;
   }
   std::string err;
-  int rc = pl->launch(*pl, ctx->stream, args, nbufs, params, params_len, &err);
+  h3::Exec ex;
+  ex.stream = ctx->stream;
+  ex.ws = ctx->ws;
+  ex.ws_bytes = ctx->ws_bytes;
+  int rc = pl->launch(*pl, ex, args, nbufs, params, params_len, &err);
   if (rc) {
     set_error(pl->name + ": " + err);
     if (e0) hipEventDestroy(e0);

@@ -378,7 +378,7 @@ __global__ __launch_bounds__(256) void widen_i8_f16(const signed char *__restric
 // Formats: WFMT 1 (q8: int8 A and W, sa[m] sw[n]), 4 (f16: half A and W), 5 (bf16), 6 (h8: half A, int8 W with
 // sw[n]; W widened to half first).
 template <int OT, int EPI, bool HAS_BIAS, int WFMT>
-int launch_gemm(const Pipeline &pl, hipStream_t stream, const Arg *a, int nargs, const void *params,
+int launch_gemm(const Pipeline &pl, const Exec &ex, const Arg *a, int nargs, const void *params,
                 uint32_t params_len, std::string *err) {
   (void)pl;
   constexpr int AT = WFMT == 1 ? A_I8 : WFMT == 5 ? A_BF16 : A_F16;
@@ -441,9 +441,14 @@ int launch_gemm(const Pipeline &pl, hipStream_t stream, const Arg *a, int nargs,
   const void *wptr = a[1].ptr;
   if constexpr (WFMT == 6) {
     // the widened weights go to the stream's scratch buffer; the product reads them with a dense row stride
-    _Float16 *wh = (_Float16 *)split_workspace(stream, (size_t)N * p.K * 2, "gemm (h8 weights)", err);
-    if (!wh) return -1;
-    hipLaunchKernelGGL(widen_i8_f16, dim3((unsigned)((p.K / 8 + 255) / 256), (unsigned)N), dim3(256), 0, stream,
+    const size_t wbytes = (size_t)N * p.K * 2;
+    if (wbytes > ex.ws_bytes) {
+      *err = "the widened h8 weights need " + std::to_string(wbytes) + " bytes of scratch, " +
+             std::to_string(ex.ws_bytes) + " are reserved (h3_reserve_workspace)";
+      return -1;
+    }
+    _Float16 *wh = (_Float16 *)ex.ws;
+    hipLaunchKernelGGL(widen_i8_f16, dim3((unsigned)((p.K / 8 + 255) / 256), (unsigned)N), dim3(256), 0, ex.stream,
                        (const signed char *)a[1].ptr, wh, p.N, p.K, p.w_stride);
     wptr = wh;
     p.w_stride = p.K;
@@ -467,7 +472,7 @@ int launch_gemm(const Pipeline &pl, hipStream_t stream, const Arg *a, int nargs,
     }
     attr_set = true;
   }
-  hipLaunchKernelGGL(kern, dim3((unsigned)(ntm * ntn)), dim3(NWG * 64), LDS_BYTES, stream, (const char *)a[0].ptr,
+  hipLaunchKernelGGL(kern, dim3((unsigned)(ntm * ntn)), dim3(NWG * 64), LDS_BYTES, ex.stream, (const char *)a[0].ptr,
                      (const char *)wptr, SM != S_NONE ? (const float *)a[2].ptr : nullptr,
                      SM == S_ROW_COL ? (const float *)a[3].ptr : nullptr, a[4].ptr,
                      HAS_BIAS ? (const float *)a[5].ptr : nullptr, EPI ? (const unsigned char *)a[6].ptr : nullptr,

@@ -66,8 +66,17 @@ struct Arg {
   uint64_t avail = 0;
 };
 
+// Where a launch runs: the stream, and the scratch memory its kernels may use (the attention tail split's
+// partial states, the h8 GEMM's widened weights). Launchers never allocate: work that needs more scratch than
+// `ws_bytes` either shrinks to fit (the attention split) or fails with a message naming the size it needs.
+struct Exec {
+  hipStream_t stream = nullptr;
+  void *ws = nullptr;
+  size_t ws_bytes = 0;
+};
+
 struct Pipeline;
-using LaunchFn = int (*)(const Pipeline &pl, hipStream_t stream, const Arg *args, int nargs, const void *params,
+using LaunchFn = int (*)(const Pipeline &pl, const Exec &ex, const Arg *args, int nargs, const void *params,
                          uint32_t params_len, std::string *err);
 
 // A selected kernel specialisation (what h3_pipeline returns).
@@ -143,10 +152,11 @@ __device__ __forceinline__ void dma4(unsigned m0, unsigned voff, __amdgpu_buffer
                : "memory", "m0");
 }
 
-// Compute units of the current device (0 if unknown), and the per-stream scratch buffer of the tail splits
-// (at least `bytes`, grown on demand, kept until the process ends; NULL with a message on failure).
+// Compute units of the current device (0 if unknown).
 int cu_count();
-void *split_workspace(hipStream_t stream, size_t bytes, const char *who, std::string *err);
+// Scratch bytes the attention launcher's tail split can use at most on a device with `cus` compute units
+// (what h3_open reserves, so that ordinary dispatches never wait for memory).
+size_t attention_workspace_max(int cus);
 
 // Helpers for macro parsing in the factories.
 bool macro_int(const Macros &m, const char *key, int def, int *out, std::string *err);

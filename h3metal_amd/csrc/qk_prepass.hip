@@ -242,7 +242,7 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kernel(const char *__restric
 int esize(int t) { return t == T_I8 ? 1 : t == T_F32 ? 4 : 2; }
 
 template <int HDIM, int IN_T, int QK_T, int V_T, bool QKROT>
-int launch_qk(const Pipeline &pl, hipStream_t stream, const Arg *a, int nargs, const void *params,
+int launch_qk(const Pipeline &pl, const Exec &ex, const Arg *a, int nargs, const void *params,
               uint32_t params_len, std::string *err) {
   (void)pl;
   if (params_len != sizeof(QkRopeParams)) {
@@ -319,7 +319,7 @@ int launch_qk(const Pipeline &pl, hipStream_t stream, const Arg *a, int nargs, c
     constexpr int P = decltype(per_const)::value;
     constexpr int SPG = PrepassShape<HDIM, P>::SPG;
     dim3 grid((unsigned)((p.M + RPW - 1) / RPW), (unsigned)((nslots + SPG - 1) / SPG));
-    hipLaunchKernelGGL((qk_norm_rope_kernel<HDIM, P, IN_T, QK_T, V_T, QKROT>), grid, dim3(256), 0, stream, a[0].ptr,
+    hipLaunchKernelGGL((qk_norm_rope_kernel<HDIM, P, IN_T, QK_T, V_T, QKROT>), grid, dim3(256), 0, ex.stream, a[0].ptr,
                        (const float *)a[1].ptr, (const float *)a[2].ptr, (const float *)a[3].ptr,
                        (const float *)a[4].ptr, a[5].ptr, a[6].ptr, a[7].ptr,
                        nargs > 9 ? (float *)a[9].ptr : nullptr, nargs > 10 ? (float *)a[10].ptr : nullptr, p);

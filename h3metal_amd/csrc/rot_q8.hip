@@ -154,7 +154,7 @@ __global__ __launch_bounds__(256) void rot_q8_kernel(const char *__restrict__ in
 int esize(int t) { return t == T_F32 ? 4 : 2; }
 
 template <int IN_T, bool OUT_HR, int MAXB>
-int launch_rot(const Pipeline &pl, hipStream_t stream, const Arg *a, int nargs, const void *params,
+int launch_rot(const Pipeline &pl, const Exec &ex, const Arg *a, int nargs, const void *params,
                uint32_t params_len, std::string *err) {
   (void)pl;
   if (params_len != sizeof(RotQParams)) {
@@ -194,10 +194,10 @@ int launch_rot(const Pipeline &pl, hipStream_t stream, const Arg *a, int nargs, 
       (!OUT_HR && !fits(2, (uint64_t)p.M * 4, "sa")))
     return -1;
   if (p.mode)
-    hipLaunchKernelGGL((rot_q8_kernel<IN_T, true, OUT_HR, MAXB>), dim3((unsigned)p.M), dim3(256), 0, stream,
+    hipLaunchKernelGGL((rot_q8_kernel<IN_T, true, OUT_HR, MAXB>), dim3((unsigned)p.M), dim3(256), 0, ex.stream,
                        a[0].ptr, a[1].ptr, OUT_HR ? nullptr : (float *)a[2].ptr, p);
   else
-    hipLaunchKernelGGL((rot_q8_kernel<IN_T, false, OUT_HR, MAXB>), dim3((unsigned)p.M), dim3(256), 0, stream,
+    hipLaunchKernelGGL((rot_q8_kernel<IN_T, false, OUT_HR, MAXB>), dim3((unsigned)p.M), dim3(256), 0, ex.stream,
                        a[0].ptr, a[1].ptr, OUT_HR ? nullptr : (float *)a[2].ptr, p);
   return 0;
 }

@@ -62,6 +62,8 @@ SIGNATURES = {
     "h3_wait": (ctypes.c_double, [ctypes.c_void_p]),
     "h3_set_profile": (None, [ctypes.c_void_p, ctypes.c_int]),
     "h3_profile_take": (ctypes.c_int, [ctypes.c_void_p, ctypes.POINTER(ctypes.c_double), ctypes.c_int]),
+    "h3_reserve_workspace": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_uint64]),
+    "h3_workspace_bytes": (ctypes.c_uint64, [ctypes.c_void_p]),
 }
 
 
@@ -116,7 +118,7 @@ class Buffer:
 
 @dataclass
 class Tensor:
-    """A typed view of (part of) a device buffer."""
+    """Element type, shape and starting byte of some device memory inside a `Buffer`."""
     buf: Buffer
     offset: int
     shape: tuple
@@ -157,7 +159,7 @@ class Tensor:
         return Tensor(self.buf, self.offset + int(offset_elems * _SIZE[self.dtype]), tuple(shape), dtype)
 
     def row(self, start: int, count: int):
-        """Rows [start, start + count) of a 2-D (or higher) contiguous tensor."""
+        """`count` leading-axis slices starting at slice `start`, for a tensor stored without gaps."""
         per = int(math.prod(self.shape[1:]))
         return Tensor(self.buf, self.offset + int(start * per * _SIZE[self.dtype]), (count,) + tuple(self.shape[1:]),
                       self.dtype)
@@ -184,7 +186,7 @@ class Gpu:
         self.working_set = lib().h3_recommended_working_set(self.ctx)
         self.max_buffer = lib().h3_max_buffer_length(self.ctx)
         self._kernels = {}
-        self.names = []  # kernel names of the dispatches recorded in profile mode
+        self.names = []  # while profiling: one name per launch, matched with its duration by profile_take()
 
     def kernel(self, file: str, fn: str, **macros) -> Kernel:
         key = (file, fn, tuple(sorted(macros.items())))
@@ -194,7 +196,6 @@ class Gpu:
             self._kernels[key] = k
         return k
 
-    # -- memory --------------------------------------------------------------------------------------------------
     def buffer(self, nbytes: int) -> Buffer:
         h = lib().h3_buffer(self.ctx, max(1, int(nbytes)))
         if not h:
@@ -216,7 +217,6 @@ class Gpu:
         t.write(np.ascontiguousarray(arr).view(_NP[dtype]).reshape(t.shape))
         return t
 
-    # -- execution -----------------------------------------------------------------------------------------------
     def launch(self, k: Kernel, grid, threads, args, params: bytes = b"", params_index: int | None = None,
                tg_mem: int = 0):
         """Launches kernel `k` with buffers `args` (Tensor, (Buffer, offset) or None) and a parameter block.
@@ -261,6 +261,16 @@ class Gpu:
         n = lib().h3_profile_take(self.ctx, out, 100000)
         names, self.names = self.names[:n], self.names[n:]
         return list(zip(names, out[:n]))
+
+    def reserve_workspace(self, nbytes: int):
+        """Grows the dispatch scratch memory to at least `nbytes` (drains the stream first when it grows), so
+        that a later launch needing that much scratch neither allocates nor waits."""
+        if lib().h3_reserve_workspace(self.ctx, int(nbytes)):
+            raise GpuError(_err())
+
+    @property
+    def workspace_bytes(self) -> int:
+        return int(lib().h3_workspace_bytes(self.ctx))
 
     def close(self):
         if self.ctx:

@@ -37,7 +37,8 @@ def attention(gpu: Gpu, q: Tensor, k: Tensor, v: Tensor, out: Tensor, *, Lq: int
               D: int, q_rows: int, k_rows: int, scale: float, causal: bool = False, causal_off: int = 0,
               wm: int = 8, bk: int = 32, seq_heads: int | None = None, seq_rows: int = 0,
               q_scale: Tensor | None = None, k_scale: Tensor | None = None, **variant):
-    """out = softmax(q k^T * scale) v per head (int8 scores when q_scale / k_scale are given).
+    """Per query head h: softmax over keys of (scale * q_i . k_j), the weights applied to the rows of v; with
+    q_scale / k_scale the scores are int8 products dequantised by the two scales.
 
     q [H][q_rows][D], k and v [KVH][k_rows][D]; out rows (h // seq_heads) * seq_rows + i, columns
     (h % seq_heads) * D, row stride seq_heads * D. wm, bk and the reference's variant flags (DB, PVORDER, VX, KPAD,
@@ -61,15 +62,20 @@ def attention(gpu: Gpu, q: Tensor, k: Tensor, v: Tensor, out: Tensor, *, Lq: int
 
 def attention_scores(gpu: Gpu, q: Tensor, k: Tensor, v: Tensor, scores: Tensor, *, Lq: int, L: int, H: int,
                      KVH: int, D: int, q_rows: int, k_rows: int, q_scale: Tensor | None = None,
-                     k_scale: Tensor | None = None, **variant):
-    """Test hook (no reference counterpart): the raw score accumulators of attention's own MFMA path,
-    scores[h][i][j] = q_i . k_j (int32 for int8 inputs, f32 otherwise), for keys j < L. With int8 inputs at
-    D=128 they come from the kernel that ops.attention would run (GROUPS=2 selects the two-group one)."""
+                     k_scale: Tensor | None = None, out: Tensor | None = None, scale: float = 1.0, **variant):
+    """Test hook (no reference counterpart): attention as ops.attention runs it, plus the raw score accumulators
+    of its MFMAs, scores[h][i][j] = q_i . k_j (int32 for int8 inputs, f32 otherwise) for keys j < L. At D = 128
+    without a causal mask the kernel that runs is ops.attention's own (same tiles, staging, tail split and
+    P V), which then also writes `out` ([Lq][H * D] rows, as ops.attention with seq_heads = H). GROUPS=2 / 3
+    select the older kernels, which write the scores only."""
     q8 = q_scale is not None
     vt = v.dtype if v.dtype in ("f16", "bf16") else "bf16"
-    kern = gpu.kernel("attention", "attention_scores", HD=D, QK8=int(q8), IN_T=OUT_DT[vt], **variant)
-    params = pack("7if3i", Lq, L, H, KVH, q_rows, k_rows, H * D, 1.0, 0, H, 0)
-    gpu.launch(kern, None, None, [q, k, v, scores, None, q_scale, k_scale], params, params_index=4)
+    if out is None:
+        out = gpu.empty((Lq, H * D), vt)
+    kern = gpu.kernel("attention", "attention_scores", HD=D, QK8=int(q8), IN_T=OUT_DT[vt], O_T=OUT_DT[out.dtype],
+                      **variant)
+    params = pack("7if3i", Lq, L, H, KVH, q_rows, k_rows, H * D, scale * LOG2E, 0, H, 0)
+    gpu.launch(kern, None, None, [q, k, v, out, None, q_scale, k_scale, scores], params, params_index=4)
 
 
 def qk_norm_rope(gpu: Gpu, qkv: Tensor, wq: Tensor | None, wk: Tensor | None, cos: Tensor | None,
@@ -95,17 +101,18 @@ def qk_norm_rope(gpu: Gpu, qkv: Tensor, wq: Tensor | None, wk: Tensor | None, co
 
 
 def _rows_kernel_cfg(D: int):
-    """SIMD-groups and rotation blocks per SIMD-group of the reference's row kernels (h3metal/ops.py:193-197);
-    passed as the NSG / MAXB specialisation, which bounds the row length (NSG * MAXB * 256 columns)."""
-    nb = D // 256
-    nsg = 8 if nb >= 8 else nb
-    return nsg, -(-nb // nsg)
+    """(NSG, MAXB) specialisation of the row kernels, chosen as in h3metal/ops.py:193-197: a row has D / 256
+    rotation blocks, spread over at most 8 groups, each taking a ceiling share (NSG * MAXB * 256 >= D)."""
+    blocks = D // 256
+    groups = min(blocks, 8)
+    return groups, (blocks + groups - 1) // groups
 
 
 def rot_q8(gpu: Gpu, x: Tensor, out: Tensor, sa: Tensor | None, M: int, D: int, *, swiglu: bool = False,
            x_stride: int | None = None, out_hr: bool = False):
-    """out = int8(rot(x)) (or of value * silu(gate) with the gates in columns D..2D-1) and its row scales;
-    with out_hr the rotated rows in half precision instead. rot multiplies every 256-column block by the
+    """Rotates each row of x (or value * silu(gate), value in columns 0..D-1 and gate in D..2D-1 when swiglu)
+    and rounds it to int8 codes with one float scale per row; out_hr keeps the rotated rows as half instead.
+    The rotation multiplies every 256-column block by the
     orthonormal 256-point Walsh-Hadamard matrix. x [M][x_stride] (f16 / bf16 / f32), out [M][D] i8 (f16 with
     out_hr), sa [M] f32."""
     if D < 256 or D % 256:
@@ -171,6 +178,8 @@ def gemm(gpu: Gpu, a: Tensor, wt: QWeight, out: Tensor, M: int, *, sa: Tensor | 
     out_t = OUT_DT[out.dtype] if epi == 0 else "float"
     k = gpu.kernel("gemm", "gemm", WFMT=FMT_ID[wt.fmt], EPI=epi, OUT_T=out_t, TM=tm, TN=tn, NSG=nsg, G=wt.G,
                    HAS_BIAS=int(wt.bias is not None), SWZ=swz)
+    if wt.fmt == "h8":
+        gpu.reserve_workspace(wt.N * wt.K * 2)  # the widened weights; grows (and waits) only the first time
     m_pad = (M + tm - 1) // tm * tm
     params = pack("8i", m_pad, wt.N, wt.K, a_stride or wt.K, c_stride or wt.N, wt.w_stride, wt.K // wt.G,
                   g_stride or wt.N)

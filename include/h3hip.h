@@ -84,6 +84,15 @@ int h3_pipeline_max_threads(void *pso);
 int h3_dispatch(h3_ctx *ctx, void *pso, const uint32_t grid[3], const uint32_t tg[3], const h3_arg *bufs,
                 int nbufs, const void *params, uint32_t params_len, int params_index, uint32_t tg_mem_bytes);
 
+// Scratch memory of the dispatches (addition, no reference counterpart: Metal
+// kernels there keep no scratch). h3_open reserves what the attention's tail
+// split needs at most, so h3_dispatch never allocates or synchronises; the h8
+// GEMM's widened weights (N * K * 2 bytes) need an explicit h3_reserve_workspace
+// first when they exceed it. h3_reserve_workspace drains the stream, then grows
+// the buffer (never shrinks it); 0 or -1. h3_workspace_bytes: the current size.
+int h3_reserve_workspace(h3_ctx *ctx, uint64_t bytes);
+uint64_t h3_workspace_bytes(h3_ctx *ctx);
+
 // Reference: src/capi.h:65-74.
 void h3_commit(h3_ctx *ctx);
 // Waits for all work on the stream. Returns the GPU seconds between the first

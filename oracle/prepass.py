@@ -20,7 +20,8 @@ float32 numpy operation, in the order the gfx950 kernel performs it:
 
 Pinning status: the rotation, signs and int8 steps are pinned by closed forms
 and invariants in tests/test_oracle.py (Hadamard matrix product, orthonormality,
-one-hot inputs, amax/127 round trip). The order of the RMS-norm sum is this
+one-hot inputs, amax/127 round trip); the order of signs and transform by the
+one-hot images s_c * H[c, :] / sqrt(n), which the swapped order fails. The order of the RMS-norm sum is this
 build's (Metal's simd_sum order is unspecified), so the norm's last-ulp
 behaviour is pinned against the gfx950 kernel and against float64 within
 tolerance only, not against the reference (parity unpinned at the last ulp).

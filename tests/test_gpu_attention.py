@@ -58,12 +58,12 @@ def run_attention(gpu, q, k, v, *, dtype, Lq, L, H, KVH, D, scale, causal=False,
 
 # -- int32 / fp32 score accumulators -------------------------------------------------------------------------------
 
-@pytest.mark.parametrize("groups", [3, 2])
+@pytest.mark.parametrize("groups", [1, 3, 2])
 @pytest.mark.parametrize("Lq,L,H,KVH,D", [(100, 100, 2, 2, 128), (77, 300, 3, 3, 128), (64, 64, 4, 1, 64),
                                           (300, 1037, 2, 1, 128), (1, 5, 1, 1, 128), (700, 449, 2, 2, 128)])
 def test_int32_scores_bit_exact(gpu, Lq, L, H, KVH, D, groups):
-    """int32 score accumulators of the kernel that runs (int8, D=128: the three-group kernel, or the two-group
-    one with GROUPS=2) equal the exact integer products."""
+    """int32 score accumulators of the kernel that runs (int8, D=128: the wave-pipelined kernel; GROUPS=3 / 2 the
+    older three- and two-group kernels; D=64 always the two-group one) equal the exact integer products."""
     rng = np.random.default_rng(Lq + L)
     qi = rng.integers(-127, 128, (H, Lq, D)).astype(np.int8)
     ki = rng.integers(-127, 128, (KVH, L, D)).astype(np.int8)
@@ -290,11 +290,49 @@ def test_config3_zimage_key_padding(gpu):
     assert err.max() < NS_MAX and err.mean() < NS_MEAN, (err.max(), err.mean(), L_txt)
 
 
+def test_config4_int32_scores_and_output_at_full_key_length(gpu):
+    """The config-4 key count (L = 16896) through the scores hook, which runs ops.attention's own kernel
+    (same tiles, LDS staging, tail split of the last round of tiles, P V and output): int32 scores of every
+    (query, key) pair of two heads bit-exact against exact integer products, and the output of the same launch
+    against float64 attention of the dequantised inputs."""
+    rng = np.random.default_rng(44)
+    H, D, Lq, L = 2, 128, 300, 16896
+    xq = rng.standard_normal((H, Lq, D)).astype(np.float32)
+    xk = rng.standard_normal((H, L, D)).astype(np.float32)
+    xq[:, :, :4] *= 20
+    xk[:, :, 5:9] *= 20
+    qi, qsc = op.quant_i8(op.rotate_f32(xq))
+    ki, ksc = op.quant_i8(op.rotate_f32(xk))
+    qi[0, 0] = -127
+    ki[0, 0] = -127  # the extreme product 128 * 127^2
+    vb = to_bf16(rng.standard_normal((H, L, D)).astype(np.float32))
+    Q, K, V = gpu.upload(qi, "i8"), gpu.upload(ki, "i8"), gpu.upload(vb, "bf16")
+    qs, ks = gpu.upload(qsc), gpu.upload(ksc)
+    S = gpu.empty((H, Lq, L), "i32")
+    O = gpu.empty((Lq, H * D), "bf16")
+    print(f"[scores] full key length Lq={Lq} L={L} H={H} (split last round)", flush=True)
+    ops.attention_scores(gpu, Q, K, V, S, Lq=Lq, L=L, H=H, KVH=H, D=D, q_rows=Lq, k_rows=L, q_scale=qs,
+                         k_scale=ks, out=O, scale=D ** -0.5)
+    gpu.wait()
+    want = oa.int_scores(qi, ki)
+    got = S.numpy()
+    assert np.array_equal(got, want), f"{(got != want).sum()} int32 scores differ"
+    ref = oa.ref_attention(qi * qsc[..., None].astype(np.float64), ki * ksc[..., None].astype(np.float64),
+                           from_bf16(vb), D ** -0.5)
+    err = np.abs(from_bf16(O.numpy()).astype(np.float64) - ref)
+    assert err.max() < NS_MAX and err.mean() < NS_MEAN, (err.max(), err.mean())
+
+
 def test_config4_int8_rotated_full_size(gpu):
     """Config 4 at full size: H=32, D=128, S=16896, outlier channels x20, rotation + int8 pre-pass, int8
-    attention with bf16 V. Checked on a seeded sample of query rows against float64 attention of the dequantised
-    int8 inputs (the reference's check_q8 convention) and, within the rotation's gain, against fp32 attention of
-    the unquantised bf16 inputs; int32 scores of sampled rows bit-exact."""
+    attention with bf16 V. On a seeded sample of query rows:
+    * against float64 attention of the dequantised int8 inputs (the reference's check_q8 convention,
+      tests/test_attention.py:89): the north-star tolerance, 2e-2 max-abs and 1e-3 mean-abs;
+    * against fp32 attention of the unquantised bf16 Q/K (heads 0 and 1): the int8 rounding itself moves the
+      output by far more than that tolerance at this outlier recipe (the oracle's dequantised attention is
+      ~0.07 relative L2 / ~0.5 max-abs away from it), so the bound is that the GPU output is no further from the
+      unquantised attention than the oracle's dequantised attention is (within 2%), and that the rotation cuts
+      the plain int8 error to below 0.6x (the reference's criterion, tests/test_qk_rotation.py:64)."""
     rng = np.random.default_rng(4)
     H, D, S = 32, 128, 16896
     x = rng.standard_normal((S, 3, H, D)).astype(np.float32)
@@ -320,6 +358,22 @@ def test_config4_int8_rotated_full_size(gpu):
     got = from_bf16(O.numpy()).astype(np.float64)[rows]
     err = np.abs(got - ref)
     assert err.max() < NS_MAX and err.mean() < NS_MEAN, (err.max(), err.mean())
+    # the unquantised reference: fp32 attention of the bf16 Q/K (heads 0, 1)
+    xf = from_bf16(xb).reshape(S, 3, H, D)
+    for h in (0, 1):
+        qf, kf = xf[:, 0, h].astype(np.float64), xf[:, 1, h].astype(np.float64)
+        fp = oa.ref_attention(qf[rows][None], kf[None], vh[h][None], D ** -0.5)
+        mine = got[:, h * D:(h + 1) * D]
+        deq = ref[:, h * D:(h + 1) * D]
+        pi, ps = op.quant_i8(xf[:, 0, h])
+        pk, pks = op.quant_i8(xf[:, 1, h])
+        plain = oa.ref_attention((pi[rows] * ps[rows, None].astype(np.float64))[None],
+                                 (pk * pks[:, None].astype(np.float64))[None], vh[h][None], D ** -0.5)
+        rel = lambda a: np.linalg.norm(a - fp) / np.linalg.norm(fp)  # noqa: E731
+        print(f"[config4 head {h}] vs unquantised: gpu rel-L2 {rel(mine):.4f} max {np.abs(mine - fp).max():.3f}; "
+              f"oracle int8 {rel(deq):.4f}; plain int8 {rel(plain):.4f}", flush=True)
+        assert rel(mine) <= 1.02 * rel(deq) + 1e-3
+        assert rel(mine) < 0.6 * rel(plain)
 
 
 def test_config5_int8_rotated_full_size(gpu):
@@ -476,8 +530,9 @@ def test_tail_split_matches_whole_tiles(gpu, q8_path):
 
 @pytest.mark.parametrize("H,KVH,Lq,L,seq", [(4, 4, 1000, 1500, None), (6, 2, 777, 2049, None), (4, 4, 300, 700, 2)])
 def test_int8_three_group_kernel_matches_ping_pong(gpu, H, KVH, Lq, L, seq):
-    """int8 scores at D=128 without a causal mask run on the three-group kernel (GROUPS=3, the default); GROUPS=2
-    keeps them on the two-group ping-pong kernel. Same inputs through both, with and without the tail split:
+    """int8 scores at D=128 without a causal mask run on the wave-pipelined kernel (GROUPS=1, the default);
+    GROUPS=3 / 2 select the three-group and two-group ping-pong kernels. Same inputs through all, with and
+    without the tail split:
     every output meets the tolerance against float64 and the kernels agree to rounding. Ragged L (a partly masked
     last key block), GQA, several 384-row query blocks per head and batched sequences (seq_heads) included."""
     rng = np.random.default_rng(H * 1000 + L)
@@ -491,7 +546,7 @@ def test_int8_three_group_kernel_matches_ping_pong(gpu, H, KVH, Lq, L, seq):
     seq_heads = seq or H
     nseq = H // seq_heads
     outs = []
-    for groups, split in ((3, 1), (3, 0), (2, 1)):
+    for groups, split in ((1, 1), (1, 0), (3, 1), (3, 0), (2, 1)):
         print(f"[attention] groups={groups} split={split} H={H} KVH={KVH} Lq={Lq} L={L} seq={seq}", flush=True)
         O = gpu.empty((nseq * qr, seq_heads * D), "f32")
         ops.attention(gpu, Q, K, V, O, Lq=Lq, L=L, H=H, KVH=KVH, D=D, q_rows=qr, k_rows=kr, scale=D ** -0.5,
@@ -505,22 +560,24 @@ def test_int8_three_group_kernel_matches_ping_pong(gpu, H, KVH, Lq, L, seq):
         got = np.concatenate([o[s * qr:s * qr + Lq, :] for s in range(nseq)], axis=1)
         err = np.abs(got - ref)
         assert err.max() < NS_MAX and err.mean() < NS_MEAN, (err.max(), err.mean())
-    assert np.abs(outs[0] - outs[2]).max() < 2e-3
-    assert np.abs(outs[1] - outs[2]).max() < 2e-3
+    for o in outs[:-1]:
+        assert np.abs(o - outs[-1]).max() < 2e-3
 
 
 def test_groups_macro_refused(gpu):
-    """GROUPS accepts 2 or 3 only (checked on the host when the pipeline is made)."""
+    """GROUPS accepts 1, 2 or 3 only (checked on the host when the pipeline is made)."""
     from h3metal_amd.gpu import GpuError
     with pytest.raises(GpuError, match="GROUPS"):
         gpu.kernel("attention", "attention", HD=128, QK8=1, IN_T="bfloat", O_T="bfloat", GROUPS=4)
 
 
 @pytest.mark.parametrize("Lq,L", [(1, 1), (5, 63), (384, 64), (385, 65), (17, 129), (700, 191)])
-def test_int8_three_group_kernel_edges(gpu, Lq, L):
-    """Edge shapes through the three-group kernel (int8, D=128, no causal mask): one query or one key, key counts
-    around the 64-key block (the last block's rows past L load as zeros and are masked), query counts around the
-    384-row tile. Checked against float64 within the north-star tolerance."""
+@pytest.mark.parametrize("groups", [1, 3])
+def test_int8_three_group_kernel_edges(gpu, Lq, L, groups):
+    """Edge shapes through the wave-pipelined (GROUPS=1) and three-group kernels (int8, D=128, no causal mask):
+    one query or one key, key counts around the 64-key block (the last block's rows past L load as zeros and are
+    masked), query counts around the 256- and 384-row tiles. Checked against float64 within the north-star
+    tolerance."""
     rng = np.random.default_rng(Lq * 1000 + L)
     H, D = 2, 128
     qr, kr = -(-Lq // 384) * 384, -(-L // 64) * 64
@@ -529,9 +586,9 @@ def test_int8_three_group_kernel_edges(gpu, Lq, L):
     v = to_bf16(rng.standard_normal((H, L, D)).astype(np.float32))
     Q, K, V = padded(gpu, qi, qr, "i8"), padded(gpu, ki, kr, "i8"), padded(gpu, v, kr, "bf16")
     O = gpu.empty((qr, H * D), "f32")
-    print(f"[attention] three-group edge Lq={Lq} L={L}", flush=True)
+    print(f"[attention] edge groups={groups} Lq={Lq} L={L}", flush=True)
     ops.attention(gpu, Q, K, V, O, Lq=Lq, L=L, H=H, KVH=H, D=D, q_rows=qr, k_rows=kr, scale=D ** -0.5,
-                  q_scale=padded(gpu, qs, qr, "f32"), k_scale=padded(gpu, ks, kr, "f32"))
+                  q_scale=padded(gpu, qs, qr, "f32"), k_scale=padded(gpu, ks, kr, "f32"), GROUPS=groups)
     gpu.wait()
     got = O.numpy().astype(np.float64)
     ref = oa.ref_attention(qi * qs[..., None].astype(np.float64), ki * ks[..., None].astype(np.float64),

@@ -41,7 +41,8 @@ def test_unknown_kernel_and_macros(gpu):
         gpu.kernel("ops", "qk_norm_rope", QKROT=1)
     # the reference's file names and tuning macros are accepted
     k = gpu.kernel("attention.metal", "attention", HD=128, WM=10, BK=32, DB=1, PVORDER=1, VX=1, QK8=1, O_T="bfloat")
-    assert k.max_threads == 768  # the three-group kernel's workgroup
+    assert k.max_threads == 256  # the wave-pipelined kernel's workgroup
+    assert gpu.kernel("attention", "attention", HD=128, QK8=1, O_T="bfloat", GROUPS=3).max_threads == 768
     assert gpu.kernel("attention", "attention", HD=128, QK8=1, O_T="bfloat", GROUPS=2).max_threads == 512
     assert gpu.kernel("attention", "attention", HD=128, QK8=1, O_T="bfloat", CAUSAL=1).max_threads == 512
 
@@ -81,3 +82,77 @@ def test_wait_time_and_profile(gpu):
     assert dt > 0 and len(prof) == 3
     assert all(t > 0 for _, t in prof) and sum(t for _, t in prof) <= dt * 1.01
     assert prof[0][0].startswith("attention:attention(")
+
+
+def test_misaligned_views_refused(gpu):
+    """Q/K/V rows are read 16 bytes at a time and O written 4 elements at a time: a view whose base breaks
+    that is refused on the host, not run."""
+    H, S, D = 2, 64, 128
+    Q = gpu.empty((H * S * D + 8,), "f16")
+    O = gpu.empty((S, H * D + 4), "f16")
+    good = Q.view((H, S, D))
+    bad = Q.view((H, S, D), offset_elems=4)  # 8 bytes in
+    with pytest.raises(GpuError, match="16-byte aligned"):
+        ops.attention(gpu, bad, good, good, O.view((S, H * D)), Lq=S, L=S, H=H, KVH=H, D=D, q_rows=S, k_rows=S,
+                      scale=0.1)
+    with pytest.raises(GpuError, match="aligned to 4 elements"):
+        ops.attention(gpu, good, good, good, O.view((S, H * D), offset_elems=1), Lq=S, L=S, H=H, KVH=H, D=D,
+                      q_rows=S, k_rows=S, scale=0.1)
+    ops.attention(gpu, good, good, good, O.view((S, H * D)), Lq=S, L=S, H=H, KVH=H, D=D, q_rows=S, k_rows=S,
+                  scale=0.1)
+    gpu.wait()
+
+
+def _int8_attention(gpu, H, S, out=None):
+    """int8 attention over zero-filled inputs (unit scales): every score 0, so the output is the mean of V."""
+    D = 128
+    Q = gpu.empty((H, S, D), "i8")
+    V = gpu.empty((H, S, D), "bf16")
+    sc = gpu.upload(np.ones((H, S), np.float32))
+    O = out if out is not None else gpu.empty((S, H * D), "bf16")
+    return lambda: ops.attention(gpu, Q, Q, V, O, Lq=S, L=S, H=H, KVH=H, D=D, q_rows=S, k_rows=S,
+                                 scale=D ** -0.5, q_scale=sc, k_scale=sc)
+
+
+def test_dispatch_neither_allocates_nor_waits(gpu):
+    """The scratch memory of the attention tail split is reserved when the context opens: a dispatch at a new
+    shape that splits its last round of tiles neither grows it nor waits for the queued work."""
+    import time
+    heavy = _int8_attention(gpu, 32, 16896)
+    warm = _int8_attention(gpu, 2, 4096)  # 22 tiles of 384 rows: a split last round
+    fresh = _int8_attention(gpu, 3, 4096)  # 33 tiles: a split of another size
+    heavy()
+    warm()
+    gpu.wait()
+    ws0 = gpu.workspace_bytes
+    assert ws0 > 0
+    t0 = time.perf_counter()
+    for _ in range(3):
+        heavy()
+    queued = time.perf_counter()
+    fresh()
+    dt = time.perf_counter() - queued
+    gpu_s = gpu.wait()
+    assert gpu.workspace_bytes == ws0
+    assert gpu_s > 5e-3, gpu_s  # three config-4-sized calls were still running during the dispatch
+    assert dt < 0.25 * gpu_s, (dt, gpu_s, queued - t0)
+
+
+def test_h8_gemm_reserves_its_scratch_outside_the_dispatch(gpu):
+    """The h8 GEMM's widened weights need N * K * 2 bytes of scratch: the launcher grows the reservation by an
+    explicit call, and a dispatch that finds too little fails with the size it needs."""
+    N, K, M = 4096, 16384, 256
+    w = gpu.empty((N, K), "i8")
+    sw = gpu.upload(np.ones(N, np.float32))
+    a = gpu.empty((M, K), "f16")
+    out = gpu.empty((M, N), "f16")
+    need = N * K * 2
+    if gpu.workspace_bytes < need:
+        k = gpu.kernel("gemm", "gemm", WFMT=6, EPI=0, OUT_T="half", TM=64, TN=128, NSG=4, G=128, HAS_BIAS=0, SWZ=1)
+        with pytest.raises(GpuError, match="bytes of scratch"):
+            gpu.launch(k, None, None, [a, w, sw, None, out, None, None, None],
+                       pack("8i", M, N, K, K, N, K, K // 128, N), params_index=8)
+    ops.gemm(gpu, a, ops.QWeight("h8", w, sw, N, K), out, M)
+    gpu.wait()
+    assert gpu.workspace_bytes >= need
+    assert (out.numpy() == 0).all()

@@ -77,6 +77,23 @@ def test_rotation_orthonormal_and_preserves_dot():
     np.testing.assert_allclose(dq, (q.astype(np.float64) * k).sum(-1), rtol=1e-5, atol=1e-4)
 
 
+def test_rotation_sign_order_pinned_by_one_hot_rows():
+    """The signs act on the INPUT channels, before the butterflies (kernels/ops.metal:424-428 flips channel c,
+    then :430-446 transform): the image of the unit vector e_c is s_c * H[c, :] / sqrt(n), with H the Sylvester
+    Hadamard matrix H[c, j] = (-1)^popcount(c & j) and s_c = -1 where popcount(c * 0x2545F491 mod 2^32) is odd,
+    both evaluated here with Python integers. The other order (signs on the outputs, H diag(s)) gives
+    s_j * H[c, j] instead and must fail this check."""
+    n = 128
+    inv = 1.0 / np.sqrt(np.float64(n))
+    sign = [(-1.0 if bin((c * 0x2545F491) & 0xFFFFFFFF).count("1") & 1 else 1.0) for c in range(n)]
+    H = np.array([[(-1.0) ** bin(c & j).count("1") for j in range(n)] for c in range(n)])
+    want = np.array([sign[c] * H[c] for c in range(n)]) * inv
+    swapped = H * np.array(sign)[None, :] * inv
+    got = op.rotate_f32(np.eye(n, dtype=np.float32)).astype(np.float64)
+    np.testing.assert_array_equal(got, want.astype(np.float32).astype(np.float64))
+    assert not np.allclose(got, swapped)  # the plausible slip is distinguishable
+
+
 def test_rotation_spreads_outlier_channel():
     """A one-hot row becomes +-1/sqrt(n) in every channel: amax drops by sqrt(n)."""
     x = np.zeros((1, 128), np.float32)
