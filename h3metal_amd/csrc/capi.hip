@@ -98,6 +98,36 @@ int cu_count() {
 
 }  // namespace h3
 
+// Scratch memory of h3_dispatch_static (the entry point that allocates nothing): a fixed array in the code
+// object's device memory, one copy per GPU, kept until the process ends. Host code must never pass the array's
+// name to a kernel (it is a host-side stand-in, not a device address): h3_open looks up each device's address
+// with hipGetSymbolAddress once, with that device current, and only that address is used.
+static __device__ __align__(256) char scratch[h3::STATIC_SCRATCH_BYTES_VALUE];
+
+namespace {
+std::mutex g_scratch_mu;
+void *g_scratch_ptr[64] = {};  // per device id
+
+// The device address of `scratch` on `device` (current), looked up on the first call; NULL with a message.
+void *static_scratch(int device, std::string *err) {
+  if (device < 0 || device >= 64) {
+    *err = "device id out of range";
+    return nullptr;
+  }
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[device]) {
+    void *ptr = nullptr;
+    hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !ptr) {
+      *err = std::string("hipGetSymbolAddress(scratch): ") + hipGetErrorString(e);
+      return nullptr;
+    }
+    g_scratch_ptr[device] = ptr;
+  }
+  return g_scratch_ptr[device];
+}
+}  // namespace
+
 struct h3_ctx {
   int device = 0;
   hipStream_t stream = nullptr;
@@ -108,6 +138,7 @@ struct h3_ctx {
   // serves every launch); sized at open for the attention split, grown only by h3_reserve_workspace
   void *ws = nullptr;
   size_t ws_bytes = 0;
+  void *static_ws = nullptr;  // this device's copy of `scratch` (h3_dispatch_static)
   // timing of the work since the last wait
   hipEvent_t t0 = nullptr, t1 = nullptr;
   bool timing = false;
@@ -176,6 +207,13 @@ h3_ctx *h3_open(const char *kernel_dir) {
     return nullptr;
   }
   ctx->ws_bytes = ws;
+  std::string err;
+  ctx->static_ws = static_scratch(ctx->device, &err);
+  if (!ctx->static_ws) {
+    set_error(err);
+    h3_close(ctx);
+    return nullptr;
+  }
   return ctx;
 }
 
@@ -324,12 +362,8 @@ void *h3_pipeline(h3_ctx *ctx, const char *file, const char *fn, const char *mac
 
 int h3_pipeline_max_threads(void *pso) { return pso ? static_cast<h3::Pipeline *>(pso)->threads : 0; }
 
-int h3_dispatch(h3_ctx *ctx, void *pso, const uint32_t grid[3], const uint32_t tg[3], const h3_arg *bufs,
-                int nbufs, const void *params, uint32_t params_len, int params_index, uint32_t tg_mem_bytes) {
-  (void)grid;
-  (void)tg;
-  (void)params_index;
-  (void)tg_mem_bytes;
+static int dispatch(h3_ctx *ctx, void *pso, const h3_arg *bufs, int nbufs, const void *params,
+                    uint32_t params_len, bool no_alloc) {
   if (!ctx) {
     set_error("dispatch without a context");
     return -1;
@@ -358,8 +392,10 @@ int h3_dispatch(h3_ctx *ctx, void *pso, const uint32_t grid[3], const uint32_t t
     if (!hip_ok(hipEventRecord(ctx->t0, ctx->stream), "hipEventRecord")) return -1;
     ctx->timing = true;
   }
+  // per-dispatch profiling creates events; the allocation-free entry point does not profile
+  const bool prof = ctx->profile && !no_alloc;
   hipEvent_t e0 = nullptr, e1 = nullptr;
-  if (ctx->profile) {
+  if (prof) {
     if (!hip_ok(hipEventCreate(&e0), "hipEventCreate") || !hip_ok(hipEventCreate(&e1), "hipEventCreate") ||
         !hip_ok(hipEventRecord(e0, ctx->stream), "hipEventRecord"))
       return -1;
@@ -367,8 +403,8 @@ int h3_dispatch(h3_ctx *ctx, void *pso, const uint32_t grid[3], const uint32_t t
   std::string err;
   h3::Exec ex;
   ex.stream = ctx->stream;
-  ex.ws = ctx->ws;
-  ex.ws_bytes = ctx->ws_bytes;
+  ex.ws = no_alloc ? ctx->static_ws : ctx->ws;
+  ex.ws_bytes = no_alloc ? h3::STATIC_SCRATCH_BYTES_VALUE : ctx->ws_bytes;
   int rc = pl->launch(*pl, ex, args, nbufs, params, params_len, &err);
   if (rc) {
     set_error(pl->name + ": " + err);
@@ -381,11 +417,29 @@ int h3_dispatch(h3_ctx *ctx, void *pso, const uint32_t grid[3], const uint32_t t
     set_error(pl->name + ": launch failed: " + hipGetErrorString(le));
     return -1;
   }
-  if (ctx->profile) {
+  if (prof) {
     hipEventRecord(e1, ctx->stream);
     ctx->prof_events.emplace_back(e0, e1);
   }
   return 0;
+}
+
+int h3_dispatch(h3_ctx *ctx, void *pso, const uint32_t grid[3], const uint32_t tg[3], const h3_arg *bufs,
+                int nbufs, const void *params, uint32_t params_len, int params_index, uint32_t tg_mem_bytes) {
+  (void)grid;
+  (void)tg;
+  (void)params_index;
+  (void)tg_mem_bytes;
+  return dispatch(ctx, pso, bufs, nbufs, params, params_len, false);
+}
+
+int h3_dispatch_static(h3_ctx *ctx, void *pso, const uint32_t grid[3], const uint32_t tg[3], const h3_arg *bufs,
+                       int nbufs, const void *params, uint32_t params_len, int params_index, uint32_t tg_mem_bytes) {
+  (void)grid;
+  (void)tg;
+  (void)params_index;
+  (void)tg_mem_bytes;
+  return dispatch(ctx, pso, bufs, nbufs, params, params_len, true);
 }
 
 void h3_commit(h3_ctx *ctx) { (void)ctx; }

@@ -75,6 +75,9 @@ struct Exec {
   size_t ws_bytes = 0;
 };
 
+// Size of the fixed scratch array that h3_dispatch_static uses instead of the context's workspace.
+constexpr size_t STATIC_SCRATCH_BYTES_VALUE = (size_t)32 << 20;
+
 struct Pipeline;
 using LaunchFn = int (*)(const Pipeline &pl, const Exec &ex, const Arg *args, int nargs, const void *params,
                          uint32_t params_len, std::string *err);

@@ -58,6 +58,9 @@ SIGNATURES = {
     "h3_dispatch": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, ctypes.POINTER(ctypes.c_uint32),
                                    ctypes.POINTER(ctypes.c_uint32), ctypes.POINTER(_Arg), ctypes.c_int,
                                    ctypes.c_void_p, ctypes.c_uint32, ctypes.c_int, ctypes.c_uint32]),
+    "h3_dispatch_static": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, ctypes.POINTER(ctypes.c_uint32),
+                                          ctypes.POINTER(ctypes.c_uint32), ctypes.POINTER(_Arg), ctypes.c_int,
+                                          ctypes.c_void_p, ctypes.c_uint32, ctypes.c_int, ctypes.c_uint32]),
     "h3_commit": (None, [ctypes.c_void_p]),
     "h3_wait": (ctypes.c_double, [ctypes.c_void_p]),
     "h3_set_profile": (None, [ctypes.c_void_p, ctypes.c_int]),
@@ -218,7 +221,7 @@ class Gpu:
         return t
 
     def launch(self, k: Kernel, grid, threads, args, params: bytes = b"", params_index: int | None = None,
-               tg_mem: int = 0):
+               tg_mem: int = 0, no_alloc: bool = False):
         """Launches kernel `k` with buffers `args` (Tensor, (Buffer, offset) or None) and a parameter block.
         grid / threads may be None: each gfx950 kernel chooses its own geometry from its parameters."""
         g = (ctypes.c_uint32 * 3)(*(list(grid or ()) + [0, 0, 0])[:3])
@@ -234,7 +237,8 @@ class Gpu:
                 arr[i].buf, arr[i].offset = a[0].handle, a[1]
         pi = n if params_index is None else params_index
         pbuf = ctypes.create_string_buffer(params, len(params)) if params else None
-        rc = lib().h3_dispatch(self.ctx, k.handle, g, t, arr, n, pbuf, len(params), pi, tg_mem)
+        entry = lib().h3_dispatch_static if no_alloc else lib().h3_dispatch
+        rc = entry(self.ctx, k.handle, g, t, arr, n, pbuf, len(params), pi, tg_mem)
         if rc:
             raise GpuError(_err())
         if self._profile:

@@ -84,6 +84,19 @@ int h3_pipeline_max_threads(void *pso);
 int h3_dispatch(h3_ctx *ctx, void *pso, const uint32_t grid[3], const uint32_t tg[3], const h3_arg *bufs,
                 int nbufs, const void *params, uint32_t params_len, int params_index, uint32_t tg_mem_bytes);
 
+// h3_dispatch without any allocation (no reference counterpart: for callers that cannot allocate device
+// memory, such as code under HIP graph capture or a serving loop that forbids it). Same arguments, checks and
+// kernels as h3_dispatch, but the scratch memory the kernels use (the attention tail split's partial states,
+// the h8 GEMM's widened weights) is a fixed 32 MiB array compiled into the library, one per GPU and held until
+// the process ends, instead of the context's workspace; it calls no hipMalloc, hipFree, event creation or other
+// allocating routine (per-dispatch profiling is skipped). Work that needs more scratch than 32 MiB: the
+// attention split shrinks to fit (down to none), an h8 GEMM with N * K * 2 > 32 MiB fails with a message.
+// Calls on one GPU share the array: dispatches through this entry point that may run at the same time on one
+// GPU (different contexts or streams) race; on one context's stream they are ordered. Nothing in the array
+// needs to start at zero (every kernel writes what it later reads).
+int h3_dispatch_static(h3_ctx *ctx, void *pso, const uint32_t grid[3], const uint32_t tg[3], const h3_arg *bufs,
+                       int nbufs, const void *params, uint32_t params_len, int params_index, uint32_t tg_mem_bytes);
+
 // Scratch memory of the dispatches (addition, no reference counterpart: Metal
 // kernels there keep no scratch). h3_open reserves what the attention's tail
 // split needs at most, so h3_dispatch never allocates or synchronises; the h8
