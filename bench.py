@@ -221,7 +221,7 @@ def main():
         "wall_ms_per_step": round(wall_s / args.steps * 1e3, 4),
         "roofline": {"bound": "mfma", "achieved": round(achieved / 1e12, 2), "peak": peak / 1e12,
                      "unit": "TFLOP/s", "frac": round(achieved / peak, 4), "traffic": traffic("attention_call"),
-                     "kernel": ("attention3_kernel (int8 QK, bf16 PV)" if path == "int8" else "attention_kernel (bf16)") + " + attention_merge",
+                     "kernel": "attention_wave_kernel (" + ("int8 QK, bf16 PV" if path == "int8" else "bf16") + ") + attention_merge",
                      "per_launch_ms": round(per_launch * 1e3, 4)},
     }
     if prepass is not None:
