@@ -48,6 +48,19 @@ constexpr int BQV = WAVE_BQ;        // query rows per workgroup (64 per wave)
 static_assert(BQV == NWV * 64, "64 query rows per wave");
 constexpr int NRV = 4;              // ring depth (blocks)
 constexpr float SUM_LIMIT = 65536.0f;
+// int8 score accumulators start from the bits of the float 1/(2 pi) (an inline constant of the MFMA's C operand,
+// so the seed costs no register): with |q . k| <= 128 * 127^2 < 2^21 the sum stays inside that float's binade
+// [2^-3, 2^-2), whose ulp is 2^-26, so the accumulator's bits ARE the float SEED_F + s * 2^-26 and
+// fma(bits, ks, -SEED_F * ks) = s * ks * 2^-26 replaces an int -> float conversion and a multiply (the 2^26 is
+// folded into the query scale). The rounding of -SEED_F * ks adds at most ks * 2^-26 (one unit of s).
+constexpr int SEED_I = 0x3E22F983;
+constexpr float SEED_F = 0.15915494f;  // the float whose bits are SEED_I
+constexpr float SEED_SCALE = 67108864.0f;  // 2^26
+#ifdef WAVE_NO_SEED
+constexpr bool SEEDED = false;
+#else
+constexpr bool SEEDED = true;
+#endif
 
 template <int QKT>
 struct CfgW {
@@ -117,6 +130,10 @@ void attention_wave_kernel(const char *__restrict__ Q, const char *__restrict__ 
     qsc[u] = p.scale;
     if constexpr (QK8) qsc[u] = q < p.Lq ? fmaxf(qs[(size_t)h * p.q_rows + q] * p.scale, FLT_MIN) : 1.0f;
   }
+  // the query scales of the main loop's seeded scores (s * ks * 2^-26)
+  float qsw[2];
+#pragma unroll
+  for (int u = 0; u < 2; u++) qsw[u] = QK8 && SEEDED ? qsc[u] * SEED_SCALE : qsc[u];
 
   int key0 = 0, Lk = p.L;
   if (unit >= 0) {
@@ -157,6 +174,19 @@ void attention_wave_kernel(const char *__restrict__ Q, const char *__restrict__ 
     // every wave loads the block's 64 scales to the same place (no wave-dependent branch or wait count)
     if constexpr (QK8) dma4(lds0 + C::SOFF + slot * BK * 4, lane * 4, rsrc(ksh, blk, 4));
   };
+  // the same loads one at a time (K and scales of block kb, V of block vb), so that they can be spread between
+  // MFMAs: load i < KDMA is a K piece, then (int8) the scales, then the V pieces
+  constexpr int NLOADS = C::KDMA + (QK8 ? 1 : 0) + C::VDMA;
+  auto stage_one = [&](int i, int kb, int vb) {
+    if (i < C::KDMA) {
+      dma16(lds0 + C::KOFF + (kb % NRV) * C::KBYTES + (i * NWV + w) * 1024, kgo[i], rsrc(Kh, kb, C::RB));
+    } else if (QK8 && i == C::KDMA) {
+      dma4(lds0 + C::SOFF + (kb % NRV) * BK * 4, lane * 4, rsrc(ksh, kb, 4));
+    } else {
+      const int r = i - C::KDMA - (QK8 ? 1 : 0);
+      dma16(lds0 + C::VOFF + (vb % NRV) * C::VBYTES + (r * NWV + w) * 1024, vgo[r], rsrc(Vh, vb, D * 2));
+    }
+  };
   auto stage_v = [&](int blk) {
     const __amdgpu_buffer_rsrc_t rv = rsrc(Vh, blk, D * 2);
 #pragma unroll
@@ -171,9 +201,12 @@ void attention_wave_kernel(const char *__restrict__ Q, const char *__restrict__ 
     for (int db = 0; db < D / 32; db++)
 #pragma unroll
       for (int i = 0; i < 16; i++) o[u][db][i] = 0.0f;
+  // l: row sums up to the previous block; la: running partial row sums (four chains per query tile)
   float m[2] = {-INFINITY, -INFINITY}, l[2] = {0.0f, 0.0f};
+  float la[2][4] = {{0.0f, 0.0f, 0.0f, 0.0f}, {0.0f, 0.0f, 0.0f, 0.0f}};
   SAcc s[2][2];    // [key tile t][query tile u]
-  VT8 pb[2][2][2]; // [t][u][16-key step within t]
+  i32x4 pb[2][2][2]; // [t][u][16-key step within t]: 8 packed 16-bit P values (whole dwords, so that the
+                     // rare path's writes merge with the common path's as whole registers)
 #pragma unroll
   for (int t = 0; t < 2; t++)
 #pragma unroll
@@ -181,7 +214,7 @@ void attention_wave_kernel(const char *__restrict__ Q, const char *__restrict__ 
 #pragma unroll
       for (int i = 0; i < 16; i++) s[t][u][i] = 0;
 #pragma unroll
-      for (int i = 0; i < 16; i++) pb[t][u][i >> 3][i & 7] = (VE)0.0f;
+      for (int i = 0; i < 8; i++) pb[t][u][i >> 2][i & 3] = 0;
     }
 
   const int krow = 16 * (l32 >> 4) + 8 * ((l32 >> 2) & 1) + 4 * ((l32 >> 3) & 1) + (l32 & 3);
@@ -202,9 +235,12 @@ void attention_wave_kernel(const char *__restrict__ Q, const char *__restrict__ 
 #pragma unroll
     for (int c = 0; c < C::NCH; c++) ka[c] = *(const i32x4 *)(Ks + kbase[c]);
   };
-  auto score_mfmas = [&](SAcc &acc, const i32x4 (&ka)[C::NCH], int u) {
+  auto score_mfmas = [&](SAcc &acc, const i32x4 (&ka)[C::NCH], int u, bool seeded) {
+    SAcc seed;
 #pragma unroll
-    for (int c = 0; c < C::NCH; c++) acc = mma_qk<QKT>(ka[c], qreg[u][c], c == 0 ? SAcc{} : acc);
+    for (int i = 0; i < 16; i++) seed[i] = seeded ? SEED_I : 0;
+#pragma unroll
+    for (int c = 0; c < C::NCH; c++) acc = mma_qk<QKT>(ka[c], qreg[u][c], c == 0 ? seed : acc);
   };
   // V operands of key tile t of block j: [16-key step][channel block]
   auto vops = [&](int j, int t, i16x8 (&va)[2][D / 32]) {
@@ -251,27 +287,26 @@ void attention_wave_kernel(const char *__restrict__ Q, const char *__restrict__ 
     }
     return x;
   };
-  auto exps = [&](const f32x16 &x, float qs_u, float nm, VT8 (&pr)[2]) {
+  auto exps = [&](const f32x16 &x, float qs_u, float nm, i32x4 (&pr)[2]) {
     float acc0 = 0.0f, acc1 = 0.0f;
 #pragma unroll
     for (int i = 0; i < 16; i += 2) {
       const float p0 = __builtin_amdgcn_exp2f(fmaf(x[i], qs_u, nm));
       const float p1 = __builtin_amdgcn_exp2f(fmaf(x[i + 1], qs_u, nm));
       const VP2 pp = {(VE)p0, (VE)p1};
-      pr[i >> 3][i & 7] = pp[0];
-      pr[i >> 3][(i & 7) + 1] = pp[1];
+      pr[i >> 3][(i & 7) >> 1] = __builtin_bit_cast(int, pp);
       if (i & 2) acc1 = sum2<VT>(pp, acc1);
       else acc0 = sum2<VT>(pp, acc0);
     }
     return acc0 + acc1;
   };
-  auto dump_scores = [&](const SAcc &acc, int j, int t, int u) {
+  auto dump_scores = [&](const SAcc &acc, int j, int t, int u, bool seeded) {
     if constexpr (DUMP) {
       const int q = q0 + 32 * u;
       if (q < p.Lq) {
         // four consecutive keys at a time, taken out of the accumulator as vectors (element-wise extraction of
         // an MFMA result vector has been miscompiled into a splat of element 0)
-        const i32x16 a = __builtin_bit_cast(i32x16, acc);
+        const i32x16 a = __builtin_bit_cast(i32x16, acc) - (seeded ? SEED_I : 0);
         const i32x4 g[4] = {__builtin_shufflevector(a, a, 0, 1, 2, 3), __builtin_shufflevector(a, a, 4, 5, 6, 7),
                             __builtin_shufflevector(a, a, 8, 9, 10, 11), __builtin_shufflevector(a, a, 12, 13, 14, 15)};
 #pragma unroll
@@ -296,6 +331,7 @@ void attention_wave_kernel(const char *__restrict__ Q, const char *__restrict__ 
     i16x8 va[8];  // index 4 * s2 + db
     i32x4 ka[C::NCH];
     f32x4 k4[4];  // keys 32 t + 16 (g / 2) + 8 hl + 4 (g % 2) + e of score group g
+    f32x4 c4[4];  // -SEED_F * k4 (int8), made in the query tile 0 sub-tile for both query tiles
   };
   auto vread = [&](int j, int t, int k) {  // V(j) operand k of key tile t
     const char *Vs = smem + C::VOFF + (j % NRV) * C::VBYTES + (32 * t + 16 * (k >> 2)) * (D * 2) + vbase[k & 3];
@@ -326,43 +362,51 @@ void attention_wave_kernel(const char *__restrict__ Q, const char *__restrict__ 
   // MFMAs and on VALU results it needs too early). When `refresh`, each operand is replaced by the one of the
   // next tile (jn, tn) right after its last use here.
   auto sub_tile = [&](Ops &op, int j, int t, int u, bool has_pv, bool has_next, bool mask, bool refresh, int jn,
-                      int tn, float &bsum) {
-    dump_scores(s[t][u], j, t, u);
+                      int tn, float (&la)[4], int st0 = 0, int stn = 0, int sj = 0) {
+    dump_scores(s[t][u], j, t, u, QK8 && SEEDED);
     const float nm = m[u] == -INFINITY ? 0.0f : -m[u];
     float xv[16];
-    float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
     int npv = 0, ns = 0;
     auto pv = [&]() {  // next P V MFMA of this sub-tile (the operand refresh also when there is none)
       const int k = npv++;
-      if (has_pv) mma_pv_acc<VT>(o[u][k & 3], op.va[k], pb[t][u][k >> 2]);
+      if (has_pv) mma_pv_acc<VT>(o[u][k & 3], op.va[k], __builtin_bit_cast(VT8, pb[t][u][k >> 2]));
       if (refresh) op.va[k] = vread(jn - 1, tn, k);
+      if (k < stn) stage_one(st0 + k, sj + 3, sj + 1);  // staging loads st0 .. st0 + stn - 1 of step sj
     };
     auto sm = [&]() {  // next score MFMA of this sub-tile
       const int c = ns++;
-      if (has_next) s[t][u] = mma_qk<QKT>(op.ka[c], qreg[u][c], c == 0 ? SAcc{} : s[t][u]);
+      SAcc seed;
+#pragma unroll
+      for (int i = 0; i < 16; i++) seed[i] = QK8 && SEEDED ? SEED_I : 0;
+      if (has_next) s[t][u] = mma_qk<QKT>(op.ka[c], qreg[u][c], c == 0 ? seed : s[t][u]);
       if (refresh) op.ka[c] = kread(jn + 1, tn, c);
     };
     // VALU stages on score group g (scores 4 g .. 4 g + 3)
-    auto cv = [&](int g) {  // int8: int32 -> float; 16-bit: the fp32 score itself
+    auto cv = [&](int g) {  // int8: the seeded accumulator's bits as a float; 16-bit: the fp32 score itself
+      // (the whole vector is cast: element-wise casts of an MFMA result have been compiled into a splat)
+      const f32x16 sf = __builtin_bit_cast(f32x16, s[t][u]);
 #pragma unroll
       for (int e = 0; e < 4; e++) {
         const int i = 4 * g + e;
-        if constexpr (QK8) xv[i] = (float)s[t][u][i];
+        if constexpr (QK8 && SEEDED) xv[i] = sf[i];
+        else if constexpr (QK8) xv[i] = (float)s[t][u][i];
         else xv[i] = s[t][u][i];
       }
     };
-    auto mu = [&](int g) {  // times the key scale (int8); keys past Lk to -inf
+    auto mu = [&](int g) {  // int8: s * ks * 2^-26; keys past Lk to -inf
+      if (QK8 && SEEDED && u == 0) op.c4[g] = op.k4[g] * -SEED_F;
 #pragma unroll
       for (int e = 0; e < 4; e++) {
         const int i = 4 * g + e;
-        if constexpr (QK8) xv[i] *= op.k4[g][e];
+        if constexpr (QK8 && SEEDED) xv[i] = fmaf(xv[i], op.k4[g][e], op.c4[g][e]);
+        else if constexpr (QK8) xv[i] *= op.k4[g][e];
         if (mask && j * BK + 32 * t + 16 * (i >> 3) + 8 * hl + (i & 7) >= Lk) xv[i] = -INFINITY;
       }
       if (QK8 && refresh && u == 1) op.k4[g] = sread(jn, tn, g);
     };
     auto fm = [&](int g) {
 #pragma unroll
-      for (int e = 0; e < 4; e++) xv[4 * g + e] = fmaf(xv[4 * g + e], qsc[u], nm);
+      for (int e = 0; e < 4; e++) xv[4 * g + e] = fmaf(xv[4 * g + e], qsw[u], nm);
     };
     auto ex = [&](int g) {
 #pragma unroll
@@ -373,9 +417,8 @@ void attention_wave_kernel(const char *__restrict__ Q, const char *__restrict__ 
       for (int e = 0; e < 4; e += 2) {
         const int i = 4 * g + e;
         const VP2 pp = {(VE)xv[i], (VE)xv[i + 1]};
-        pb[t][u][i >> 3][i & 7] = pp[0];
-        pb[t][u][i >> 3][(i & 7) + 1] = pp[1];
-        acc[(g & 1) * 2 + (e >> 1)] = sum2<VT>(pp, acc[(g & 1) * 2 + (e >> 1)]);
+        pb[t][u][i >> 3][(i & 7) >> 1] = __builtin_bit_cast(int, pp);
+        la[(g & 1) * 2 + (e >> 1)] = sum2<VT>(pp, la[(g & 1) * 2 + (e >> 1)]);
       }
     };
 #define SB __builtin_amdgcn_sched_barrier(0)
@@ -392,7 +435,6 @@ void attention_wave_kernel(const char *__restrict__ Q, const char *__restrict__ 
       sm(); SB; sm(); pk(2); SB; sm(); SB; sm(); pk(3); SB; sm(); SB;
     }
 #undef SB
-    bsum += (acc[0] + acc[1]) + (acc[2] + acc[3]);
   };
 
   // Step j: P V of block j - 1, softmax of block j, scores of block j + 1. The barrier sits before the last
@@ -400,22 +442,52 @@ void attention_wave_kernel(const char *__restrict__ Q, const char *__restrict__ 
   // step, and the last sub-tile reads the first operands of the next step, all of which landed and were
   // published by that barrier. Ring slots (4 deep): K(j + 3) replaces K(j - 1), last read in step j - 1's
   // recompute; V(j + 1) replaces V(j - 3); scales(j + 3) replace scales(j - 1).
+#ifdef WAVE_TIMING
+  // timing-only builds: shader-clock ticks per phase of the step, written to the scores buffer at the end
+  unsigned long long tph[6] = {0, 0, 0, 0, 0, 0}, tlast = 0;
+  auto tick = [&](int k) {
+    const unsigned long long now = __builtin_amdgcn_s_memtime();
+    if (k >= 0) tph[k] += now - tlast;
+    tlast = now;
+  };
+#else
+  auto tick = [](int) {};
+#endif
   auto step = [&](Ops &op, int j, bool has_pv, bool has_next, bool mask) {
-    float bs[2] = {0.0f, 0.0f};
-    sub_tile(op, j, 0, 0, has_pv, has_next, mask, false, 0, 0, bs[0]);
-    sub_tile(op, j, 0, 1, has_pv, has_next, mask, true, j, 1, bs[1]);
-    sub_tile(op, j, 1, 0, has_pv, has_next, mask, false, 0, 0, bs[0]);
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this wave's loads of the previous step
+    tick(-1);
+    // V of block j + 1 replaces V(j - 3), last read in step j - 2, before the previous barrier: with int8
+    // scores its loads are spread over the first three sub-tiles (measured faster; with 16-bit scores, whose
+    // sub-tiles read twice the K operands, slower). K and scales of block j + 3 replace those of block j - 1
+    // (read up to step j - 1's recompute) and wait for this step's barrier.
+    constexpr int KS = C::KDMA + (QK8 ? 1 : 0);  // K and scale loads come first in stage_one's order
+    constexpr int VE0 = QK8 ? C::VDMA : 0;       // V loads issued before the barrier
+    sub_tile(op, j, 0, 0, has_pv, has_next, mask, false, 0, 0, la[0], KS, QK8 ? 2 : 0, j);
+    tick(0);
+    sub_tile(op, j, 0, 1, has_pv, has_next, mask, true, j, 1, la[1], KS + 2, QK8 ? 1 : 0, j);
+    tick(1);
+    sub_tile(op, j, 1, 0, has_pv, has_next, mask, false, 0, 0, la[0], KS + 3, QK8 ? 1 : 0, j);
+    tick(2);
+    // block j's row sums are the growth of the running partial sums; query tile 0's are complete here. A sum
+    // above SUM_LIMIT (or NaN) means a score far above the reference maximum: the block is recomputed below
+    float tot[2];
+    tot[0] = (la[0][0] + la[0][1]) + (la[0][2] + la[0][3]);
+    bool bad = !(tot[0] - l[0] <= SUM_LIMIT);
+    // this wave's loads of the previous step (this step's V loads, the newest, may still be in flight)
+    static_assert(C::VDMA == 4, "V loads per wave and step");
+    if constexpr (QK8) asm volatile("s_waitcnt vmcnt(4)" ::: "memory");
+    else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
-    stage_k(j + 3);
-    stage_v(j + 1);
-    sub_tile(op, j, 1, 1, has_pv, has_next, mask, true, j + 1, 0, bs[1]);
-    // rare: a score far above the reference maximum, or the first valid keys of a row: recompute block j's
-    // P with the exact maximum
-    bool bad = false;
-#pragma unroll
-    for (int u = 0; u < 2; u++) bad = bad || !(bs[u] <= SUM_LIMIT) || m[u] == -INFINITY;
-    if (__builtin_expect(__any(bad), 0)) {
+    tick(3);
+    sub_tile(op, j, 1, 1, has_pv, has_next, mask, true, j + 1, 0, la[1], 0, KS + (C::VDMA - VE0), j);
+    tick(4);
+    tot[1] = (la[1][0] + la[1][1]) + (la[1][2] + la[1][3]);
+    bad = bad | !(tot[1] - l[1] <= SUM_LIMIT);
+#ifdef WAVE_NO_CHECK
+    bad = false;
+#endif
+    // rare: a score far above the reference maximum, or the first block (no maximum yet; it always holds
+    // valid keys, so m is finite after it): recompute block j's P with the exact maximum
+    if (__builtin_expect(j == 0 || __builtin_amdgcn_ballot_w64(bad) != 0, 0)) {
       o_fence(o);  // P V MFMAs of this step may still be writing O
 #pragma unroll
       for (int u = 0; u < 2; u++) {
@@ -429,7 +501,7 @@ void attention_wave_kernel(const char *__restrict__ Q, const char *__restrict__ 
           f32x4 k4[2][2];
           if constexpr (QK8) kscales(j, t, k4);
           SAcc acc;
-          score_mfmas(acc, ka, u);
+          score_mfmas(acc, ka, u, false);
           xs[t] = to_x(acc, k4, j, t, mask);
 #pragma unroll
           for (int i = 0; i < 16; i++) bmax = fmaxf(bmax, xs[t][i]);
@@ -444,12 +516,15 @@ void attention_wave_kernel(const char *__restrict__ Q, const char *__restrict__ 
 #pragma unroll
           for (int i = 0; i < 16; i++) o[u][db][i] *= f;
         const float nm = mn == -INFINITY ? 0.0f : -mn;
-        bs[u] = exps(xs[0], qsc[u], nm, pb[0][u]) + exps(xs[1], qsc[u], nm, pb[1][u]);
+        tot[u] = l[u] + (exps(xs[0], qsc[u], nm, pb[0][u]) + exps(xs[1], qsc[u], nm, pb[1][u]));
+        la[u][0] = tot[u];
+        la[u][1] = la[u][2] = la[u][3] = 0.0f;
       }
       asm volatile("s_nop 2" ::: "memory");  // VALU writes of O before the next MFMA reads it
     }
-    l[0] += bs[0];
-    l[1] += bs[1];
+    l[0] = tot[0];
+    l[1] = tot[1];
+    tick(5);
   };
 
   if (nblk > 0) {
@@ -465,7 +540,7 @@ void attention_wave_kernel(const char *__restrict__ Q, const char *__restrict__ 
       for (int t = 0; t < 2; t++) {
         kops(0, t, ka);
 #pragma unroll
-        for (int u = 0; u < 2; u++) score_mfmas(s[t][u], ka, u);
+        for (int u = 0; u < 2; u++) score_mfmas(s[t][u], ka, u, QK8 && SEEDED);
       }
     }
     Ops op;
@@ -485,12 +560,18 @@ void attention_wave_kernel(const char *__restrict__ Q, const char *__restrict__ 
 #pragma unroll
       for (int u = 0; u < 2; u++)
 #pragma unroll
-        for (int k = 0; k < 8; k++) mma_pv_acc<VT>(o[u][k & 3], op.va[k], pb[t][u][k >> 2]);
+        for (int k = 0; k < 8; k++) mma_pv_acc<VT>(o[u][k & 3], op.va[k], __builtin_bit_cast(VT8, pb[t][u][k >> 2]));
     }
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // loads past the last block land before the exit
     o_fence(o);  // inside the branch: no copy of O may come between the last MFMA and the fence
   }
 
+#ifdef WAVE_TIMING
+  if (lane == 0) {
+    long long *tp = (long long *)dump + ((size_t)blockIdx.x * NWV + w) * 8;
+    for (int k = 0; k < 6; k++) tp[k] = (long long)tph[k];
+  }
+#endif
 #pragma unroll
   for (int u = 0; u < 2; u++) {
     const int q = q0 + 32 * u;
@@ -547,7 +628,12 @@ int launch_attention_wave(int qkt, int vt, int ot, bool dump, const Exec &ex, co
     const long ngroups = sp.s ? (long)sp.nfull + (ntiles - sp.nfull) * sp.s : ntiles;
     hipLaunchKernelGGL(kern, dim3((unsigned)ngroups), dim3(NWV * 64), lds, ex.stream, args[0].ptr, args[1].ptr,
                        args[2].ptr, args[3].ptr, (const float *)args[5].ptr, (const float *)args[6].ptr,
-                       dump ? (int *)args[7].ptr : nullptr, p, nqb, sp);
+#ifdef WAVE_TIMING
+                       (int *)args[7].ptr,
+#else
+                       dump ? (int *)args[7].ptr : nullptr,
+#endif
+                       p, nqb, sp);
     if (sp.s) {
       const int rows = (int)(ntiles - sp.nfull) * BQV;
       switch (ot) {
