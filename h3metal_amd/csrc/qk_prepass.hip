@@ -26,8 +26,8 @@
 // consecutive channels per lane: PER = 8 (16-byte loads of 16-bit rows; 16
 // lanes per head at HDIM 128) whenever the rotary pairs (c, c + rot/2) stay
 // lane-aligned (rot/2 a multiple of 8), else the reference's HDIM / 32. Every
-// cross-lane step stays inside the group and runs on DPP / ds_swizzle (no LDS
-// memory traffic). A workgroup of 256 threads covers 4 waves' groups of slots
+// cross-lane step stays inside the group and runs on DPP lane patterns at 16
+// lanes per slot (ds_swizzle at other shapes; no LDS memory traffic). A workgroup of 256 threads covers 4 waves' groups of slots
 // of 8 consecutive rows; each wave issues all 8 rows' loads before processing
 // them, so enough bytes are in flight to stream HBM, and a slot's 8 scales are
 // stored together. The kernel is HBM-bound: one read of the rows, one write of
@@ -68,6 +68,44 @@ struct PrepassShape {
   static_assert(LPS >= RPW && LPS <= 32 && (LPS & (LPS - 1)) == 0, "lane group");
 };
 
+// Channel groups and lanes. With 16 lanes per slot the group g (channels 8 g .. 8 g + 7) sits in lane
+// L(g) = g0 ^ 2 g1 ^ 7 g2 ^ 8 g3 (g_b the bits of g): the partner along group bit 0, 1, 2, 3 is then lane L ^ 1,
+// ^ 2, ^ 7, ^ 8 -- all four DPP lane patterns within a 16-lane row (quad_perm, row_half_mirror, row_ror:8), so
+// every cross-lane step of the transform and of the reductions is one VALU instruction with no LDS traffic.
+// Other lane counts keep g = lane.
+template <int LPS>
+__device__ __forceinline__ int group_of_lane(int l) {
+  if constexpr (LPS != 16) return l;
+  const int g2 = (l >> 2) & 1, r = l ^ (7 * g2);
+  return (r & 1) | (r & 2) | (g2 << 2) | (r & 8);
+}
+template <int LPS>
+__device__ __forceinline__ int lane_of_group(int g) {
+  if constexpr (LPS != 16) return g;
+  return (g & 1) ^ (g & 2) ^ (7 * ((g >> 2) & 1)) ^ (g & 8);
+}
+// the value of the lane whose group differs in group bit B
+template <int LPS, int B>
+__device__ __forceinline__ float gshfl(float v) {
+  if constexpr (LPS == 16 && B == 4)
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x141, 0xF, 0xF, true));
+  else return xshfl<B>(v);
+}
+// one cross-lane Hadamard stage along group bit B (see hadamard_lane_stage for the sign convention)
+template <int LPS, int B, int N>
+__device__ __forceinline__ void group_stage(float (&v)[N], float c) {
+  if constexpr (LPS == 16 && B == 4) {
+    asm volatile("s_nop 1");
+#pragma unroll
+    for (int i = 0; i < N; i++)
+      asm volatile("v_fmac_f32_dpp %0, %0, %1 row_half_mirror row_mask:0xf bank_mask:0xf bound_ctrl:1"
+                   : "+v"(v[i])
+                   : "v"(c));
+  } else {
+    hadamard_lane_stage<B>(v, c);
+  }
+}
+
 template <int HDIM, int PER, int IN_T, int QK_T, int V_T, bool QKROT>
 __global__ __launch_bounds__(256) void qk_norm_rope_kernel(const char *__restrict__ in, const float *__restrict__ wq,
                                                             const float *__restrict__ wk,
@@ -83,15 +121,18 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kernel(const char *__restric
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int l32 = lane & (LPS - 1);  // lane within the slot's group
   const int gbase = lane & ~(LPS - 1);  // first lane of the group
+  const int g = group_of_lane<LPS>(l32);  // this lane's channel group: channels g * PER .. g * PER + PER - 1
   const int slot = blockIdx.y * SH::SPG + w * (64 / LPS) + lane / LPS;
+  const int m0 = blockIdx.x * RPW;
   const int nslots = p.Hq + p.Hk + p.Hv;
   if (slot >= nslots) return;  // whole lane groups only; no cross-lane step leaves a group
-  const int m0 = blockIdx.x * RPW;
   const int nr = min(RPW, p.M - m0);
+  // outputs are streamed out with nontemporal stores (nothing in this kernel reads them again; measured +6%)
+  auto st = [](auto *dst, auto val) { __builtin_nontemporal_store(val, dst); };
 
   IV xin[RPW];
   {
-    const IE *src = (const IE *)in + (size_t)m0 * p.in_stride + (size_t)slot * HDIM + l32 * PER;
+    const IE *src = (const IE *)in + (size_t)m0 * p.in_stride + (size_t)slot * HDIM + g * PER;
 #pragma unroll
     for (int r = 0; r < RPW; r++) xin[r] = *(const IV *)(src + (size_t)min(r, nr - 1) * p.in_stride);
   }
@@ -103,12 +144,12 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kernel(const char *__restric
     return ((size_t)sq * heads + h) * p.out_rows + r;
   };
   float keep = 1.0f;  // lane l32 < nr: the scale of row m0 + l32
-  // QKROT's fixed signs: channel c = l32 * PER + i is negated when popcount(c * 0x2545F491) is odd (its sign
+  // QKROT's fixed signs: channel c = g * PER + i is negated when popcount(c * 0x2545F491) is odd (its sign
   // bit, flipped by an xor; computed once per lane)
   unsigned sbit[PER];
 #pragma unroll
   for (int i = 0; i < PER; i++)
-    sbit[i] = (__builtin_popcount((unsigned)(l32 * PER + i) * 0x2545F491u) & 1u) ? 0x80000000u : 0u;
+    sbit[i] = (__builtin_popcount((unsigned)(g * PER + i) * 0x2545F491u) & 1u) ? 0x80000000u : 0u;
 
 #pragma unroll
   for (int rr = 0; rr < RPW; rr++) {
@@ -123,13 +164,14 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kernel(const char *__restric
         float ss = v[0] * v[0];
 #pragma unroll
         for (int i = 1; i < PER; i++) ss = ss + v[i] * v[i];
-        if constexpr (LPS > 16) ss = ss + xshfl<16>(ss);
-        if constexpr (LPS > 8) ss = ss + xshfl<8>(ss);
-        ss = ss + xshfl<4>(ss);
-        ss = ss + xshfl<2>(ss);
-        ss = ss + xshfl<1>(ss);
+        // over the groups in halving strides (the partner of group g is g ^ stride)
+        if constexpr (LPS > 16) ss = ss + gshfl<LPS, 16>(ss);
+        if constexpr (LPS > 8) ss = ss + gshfl<LPS, 8>(ss);
+        ss = ss + gshfl<LPS, 4>(ss);
+        ss = ss + gshfl<LPS, 2>(ss);
+        ss = ss + gshfl<LPS, 1>(ss);
         const float inv = 1.0f / sqrtf(ss / (float)HDIM + p.eps);
-        const float *wv = (isq ? wq : wk) + l32 * PER;
+        const float *wv = (isq ? wq : wk) + g * PER;
 #pragma unroll
         for (int i = 0; i < PER; i++) v[i] = (v[i] * inv) * wv[i];
       }
@@ -137,13 +179,13 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kernel(const char *__restric
         const int r = m % p.seq_len;
         const int half_rot = p.rot / 2;
         const int lanes = half_rot / PER;  // lanes holding the first half of the rotated channels
-        const int src_lane = l32 < lanes ? l32 + lanes : (l32 < 2 * lanes ? l32 - lanes : l32);
+        const int src_group = g < lanes ? g + lanes : (g < 2 * lanes ? g - lanes : g);
         float pv[PER];
 #pragma unroll
-        for (int i = 0; i < PER; i++) pv[i] = __shfl(v[i], gbase + src_lane);
-        if (l32 < 2 * lanes) {
-          const bool first = l32 < lanes;
-          const int base = (first ? l32 : l32 - lanes) * PER;  // pair index of v[0]
+        for (int i = 0; i < PER; i++) pv[i] = __shfl(v[i], gbase + lane_of_group<LPS>(src_group));
+        if (g < 2 * lanes) {
+          const bool first = g < lanes;
+          const int base = (first ? g : g - lanes) * PER;  // pair index of v[0]
           const float *c = cs + (size_t)r * half_rot + base;
           const float *s = sn + (size_t)r * half_rot + base;
 #pragma unroll
@@ -166,10 +208,10 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kernel(const char *__restric
         }
         // across lanes: channel c pairs with c ^ (ls * PER), stages in increasing bit order; the lower channel
         // becomes a + b, the upper one a - b (a the lower channel's value); each lane ends with its values
-        // times (-1)^popcount(l32) (hadamard_lane_stage)
+        // times (-1)^popcount(g) (hadamard_lane_stage)
         auto stage = [&](auto ls_const) {
           constexpr int LS = decltype(ls_const)::value;
-          hadamard_lane_stage<LS>(v, (l32 & LS) ? -1.0f : 1.0f);
+          group_stage<LPS, LS>(v, (g & LS) ? -1.0f : 1.0f);
         };
         stage(std::integral_constant<int, 1>{});
         stage(std::integral_constant<int, 2>{});
@@ -178,7 +220,7 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kernel(const char *__restric
         if constexpr (LPS > 16) stage(std::integral_constant<int, 16>{});
         // the sign carried by the lane goes into the final scale (an exact sign change of the same product)
         constexpr float rn = (float)inv_sqrt_hdim<HDIM>();
-        const float rns = (__builtin_popcount(l32) & 1) ? -rn : rn;
+        const float rns = (__builtin_popcount(g) & 1) ? -rn : rn;
 #pragma unroll
         for (int i = 0; i < PER; i++) v[i] *= rns;
       }
@@ -186,11 +228,11 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kernel(const char *__restric
         float amax = 0.0f;
 #pragma unroll
         for (int i = 0; i < PER; i++) amax = fmaxf(amax, fabsf(v[i]));
-        if constexpr (LPS > 16) amax = fmaxf(amax, xshfl<16>(amax));
-        if constexpr (LPS > 8) amax = fmaxf(amax, xshfl<8>(amax));
-        amax = fmaxf(amax, xshfl<4>(amax));
-        amax = fmaxf(amax, xshfl<2>(amax));
-        amax = fmaxf(amax, xshfl<1>(amax));
+        if constexpr (LPS > 16) amax = fmaxf(amax, gshfl<LPS, 16>(amax));
+        if constexpr (LPS > 8) amax = fmaxf(amax, gshfl<LPS, 8>(amax));
+        amax = fmaxf(amax, gshfl<LPS, 4>(amax));
+        amax = fmaxf(amax, gshfl<LPS, 2>(amax));
+        amax = fmaxf(amax, gshfl<LPS, 1>(amax));
         const float scale = amax > 0.0f ? amax / 127.0f : 1.0f;
         const float rs = __builtin_amdgcn_rcpf(scale);  // 1 ulp
         typedef typename VecOf<PER, signed char>::type CV;
@@ -211,7 +253,7 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kernel(const char *__restric
 #pragma unroll
           for (int i = 0; i < PER; i++) codes[i] = (signed char)(int)rintf(v[i] / scale);
         }
-        *(CV *)((isq ? Qo : Ko) + hrow * HDIM + l32 * PER) = codes;
+        st((CV *)((isq ? Qo : Ko) + hrow * HDIM + g * PER), codes);
         if (l32 == rr) keep = scale;
       } else {
         using OE = typename Elem<QK_T>::type;
@@ -219,18 +261,18 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kernel(const char *__restric
         OV out;
 #pragma unroll
         for (int i = 0; i < PER; i++) out[i] = (OE)v[i];
-        *(OV *)((isq ? Qo : Ko) + (hrow * HDIM + l32 * PER) * sizeof(OE)) = out;
+        st((OV *)((isq ? Qo : Ko) + (hrow * HDIM + g * PER) * sizeof(OE)), out);
       }
     } else {
       using OE = typename Elem<V_T>::type;
       typedef typename VecOf<PER, OE>::type OV;
       if constexpr (V_T == IN_T) {
-        *(OV *)(Vo + (hrow * HDIM + l32 * PER) * sizeof(OE)) = xin[rr];  // same type: a plain copy
+        st((OV *)(Vo + (hrow * HDIM + g * PER) * sizeof(OE)), xin[rr]);  // same type: a plain copy
       } else {
         OV out;
 #pragma unroll
         for (int i = 0; i < PER; i++) out[i] = (OE)v[i];
-        *(OV *)(Vo + (hrow * HDIM + l32 * PER) * sizeof(OE)) = out;
+        st((OV *)(Vo + (hrow * HDIM + g * PER) * sizeof(OE)), out);
       }
     }
   }
