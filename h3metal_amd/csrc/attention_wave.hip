@@ -43,6 +43,16 @@ __device__ __forceinline__ void o_fence(f32x16 (&o)[2][4]) {
                  "+a"(o[1][2]), "+a"(o[1][3]));
 }
 
+// First int8 score MFMA of a chain, accumulating onto the seed: the bits of 1/(2 pi) are an inline constant of
+// the srcC operand (no registers, no moves). Assembly, because the builtin materialises the constant vector in
+// registers. The next MFMA of the chain (a builtin of the same opcode) reads the result as its srcC, which the
+// matrix unit forwards back to back; nothing else reads it (checked by h3metal_amd/isa_check.py).
+__device__ __forceinline__ i32x16 mma_i8_seeded(i32x4 a, i32x4 b) {
+  i32x16 d;
+  asm volatile("v_mfma_i32_32x32x32_i8 %0, %1, %2, 0x3e22f983" : "=v"(d) : "a"(a), "a"(b));
+  return d;
+}
+
 constexpr int NWV = 4;              // waves per workgroup
 constexpr int BQV = WAVE_BQ;        // query rows per workgroup (64 per wave)
 static_assert(BQV == NWV * 64, "64 query rows per wave");
@@ -240,7 +250,15 @@ void attention_wave_kernel(const char *__restrict__ Q, const char *__restrict__ 
 #pragma unroll
     for (int i = 0; i < 16; i++) seed[i] = seeded ? SEED_I : 0;
 #pragma unroll
-    for (int c = 0; c < C::NCH; c++) acc = mma_qk<QKT>(ka[c], qreg[u][c], c == 0 ? seed : acc);
+    for (int c = 0; c < C::NCH; c++) {
+      if constexpr (QK8 && SEEDED) {
+        if (c == 0 && seeded) {
+          acc = mma_i8_seeded(ka[0], qreg[u][0]);
+          continue;
+        }
+      }
+      acc = mma_qk<QKT>(ka[c], qreg[u][c], c == 0 ? seed : acc);
+    }
   };
   // V operands of key tile t of block j: [16-key step][channel block]
   auto vops = [&](int j, int t, i16x8 (&va)[2][D / 32]) {
@@ -378,7 +396,14 @@ void attention_wave_kernel(const char *__restrict__ Q, const char *__restrict__ 
       SAcc seed;
 #pragma unroll
       for (int i = 0; i < 16; i++) seed[i] = QK8 && SEEDED ? SEED_I : 0;
-      if (has_next) s[t][u] = mma_qk<QKT>(op.ka[c], qreg[u][c], c == 0 ? seed : s[t][u]);
+      if (has_next) {
+        if constexpr (QK8 && SEEDED) {
+          if (c == 0) s[t][u] = mma_i8_seeded(op.ka[0], qreg[u][0]);
+          else s[t][u] = mma_qk<QKT>(op.ka[c], qreg[u][c], s[t][u]);
+        } else {
+          s[t][u] = mma_qk<QKT>(op.ka[c], qreg[u][c], c == 0 ? seed : s[t][u]);
+        }
+      }
       if (refresh) op.ka[c] = kread(jn + 1, tn, c);
     };
     // VALU stages on score group g (scores 4 g .. 4 g + 3)
@@ -567,10 +592,13 @@ void attention_wave_kernel(const char *__restrict__ Q, const char *__restrict__ 
   }
 
 #ifdef WAVE_TIMING
+  // the output's first bytes carry the ticks (workgroup b, wave w at 64 (NWV b + w)); no output is written
   if (lane == 0) {
-    long long *tp = (long long *)dump + ((size_t)blockIdx.x * NWV + w) * 8;
+    long long *tp = (long long *)O + ((size_t)blockIdx.x * NWV + w) * 8;
     for (int k = 0; k < 6; k++) tp[k] = (long long)tph[k];
+    tp[6] = nblk;
   }
+  return;
 #endif
 #pragma unroll
   for (int u = 0; u < 2; u++) {
@@ -628,11 +656,7 @@ int launch_attention_wave(int qkt, int vt, int ot, bool dump, const Exec &ex, co
     const long ngroups = sp.s ? (long)sp.nfull + (ntiles - sp.nfull) * sp.s : ntiles;
     hipLaunchKernelGGL(kern, dim3((unsigned)ngroups), dim3(NWV * 64), lds, ex.stream, args[0].ptr, args[1].ptr,
                        args[2].ptr, args[3].ptr, (const float *)args[5].ptr, (const float *)args[6].ptr,
-#ifdef WAVE_TIMING
-                       (int *)args[7].ptr,
-#else
                        dump ? (int *)args[7].ptr : nullptr,
-#endif
                        p, nqb, sp);
     if (sp.s) {
       const int rows = (int)(ntiles - sp.nfull) * BQV;

@@ -3,7 +3,8 @@ cannot see there (its own builtin MFMAs it protects itself):
 
 * an access by any other instruction to the destination (accumulator) registers of an inline-assembly MFMA
   within 18 wait states after it (a 16-pass XDL result is written that late; reading earlier sees the old
-  value, writing earlier is overwritten by it);
+  value, writing earlier is overwritten by it), except an MFMA of the same opcode whose srcC is exactly that
+  destination (back-to-back accumulation, which the matrix unit forwards without wait states);
 * a VALU write of a register that an MFMA reads, within 2 wait states before that MFMA.
 
 The scan is straight-line over each function (a conservative approximation across branches: pending results
@@ -32,6 +33,7 @@ def scan(text: str, name: str = "<asm>") -> list[str]:
     problems = []
     pending: dict = {}  # register -> wait states still to go after an inline-assembly MFMA wrote it
     recent: dict = {}   # register -> wait states since a VALU wrote it
+    asm_dst: dict = {}  # register -> (opcode, destination operand) of the inline-assembly MFMA that wrote it
     in_asm = False
     for ln, line in enumerate(text.split("\n"), 1):
         s = line.strip()
@@ -44,6 +46,7 @@ def scan(text: str, name: str = "<asm>") -> list[str]:
         if s.endswith(":") and not s.startswith((".", ";")) and not s.startswith(".LBB"):
             pending.clear()
             recent.clear()
+            asm_dst.clear()
             continue
         if not s or s.startswith((".", ";", "//")):
             continue
@@ -55,9 +58,25 @@ def scan(text: str, name: str = "<asm>") -> list[str]:
             for r in set().union(*[_regs(a) for a in args[1:]]):
                 if r in recent and recent[r] < VALU_TO_MFMA and r not in dst:
                     problems.append(f"{name}:{ln}: VALU write of {r} {recent[r]} wait states before: {s}")
+            # an MFMA of the same opcode that accumulates onto exactly the registers an inline-assembly MFMA wrote
+            # (srcC = that vdst) needs no wait states (the matrix unit forwards the result); every other access
+            # of pending registers is a hazard
+            src_c = args[3] if len(args) > 3 else ""
+            c_regs = _regs(src_c)
+            chained = bool(c_regs) and all(r in pending and asm_dst.get(r) == (op, src_c) for r in c_regs)
+            used = set().union(*[_regs(a) for a in args[1:3]]) | (set() if chained else c_regs)
+            hit = sorted(r for r in used if pending.get(r, 0) > 0)
+            if hit:
+                problems.append(f"{name}:{ln}: {op} reads {hit[0]} {XDL_WAIT - pending[hit[0]]} wait states "
+                                f"after its MFMA: {s}")
+            if chained and args[0] == src_c:
+                for r in c_regs:
+                    pending.pop(r, None)
+                    asm_dst.pop(r, None)
             if in_asm:
                 for r in dst:
                     pending[r] = XDL_WAIT
+                    asm_dst[r] = (op, args[0])
         elif not op.startswith("s_"):
             used = set().union(*[_regs(a) for a in args]) if args else set()
             hit = sorted(r for r in used if pending.get(r, 0) > 0)
