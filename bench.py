@@ -132,6 +132,31 @@ def cpu_baseline(kw, cfg, L, budget_s=20.0):
                       f"extrapolated x{H} heads = {total:.2f} s per call"}
 
 
+def copy_rates(sizes, reps=10):
+    """Bytes per second of a plain device copy moving the same traffic as each of `sizes` (n / 2 read, n / 2
+    written): the HBM rate a streaming kernel of that size can reach on this part (torch's copy kernel). Run in a
+    child process: torch brings its own HIP runtime, which must not share a process with this library's."""
+    import subprocess
+    code = ("import json, sys, torch\n"
+            "out = []\n"
+            "for nb in json.loads(sys.argv[1]):\n"
+            "    n = nb // 2\n"
+            "    a = torch.ones(n, dtype=torch.uint8, device='cuda'); b = torch.empty_like(a)\n"
+            "    for _ in range(3): b.copy_(a)\n"
+            "    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)\n"
+            f"    e0.record()\n    for _ in range({reps}): b.copy_(a)\n"
+            "    e1.record(); torch.cuda.synchronize()\n"
+            f"    out.append(2 * n / (e0.elapsed_time(e1) / {reps} / 1e3))\n"
+            "    del a, b; torch.cuda.empty_cache()\n"
+            "print(json.dumps(out))\n")
+    try:
+        r = subprocess.run([sys.executable, "-c", code, json.dumps([int(x) for x in sizes])], capture_output=True,
+                           text=True, timeout=300)
+        return json.loads(r.stdout.strip().splitlines()[-1])
+    except Exception:  # noqa: BLE001 -- the yardstick is optional
+        return [None] * len(sizes)
+
+
 def traffic(kernel, cfg="c4"):
     """HBM bytes per launch of `kernel` at `cfg`, from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE runs
     (profiles/hbm_traffic_c4.md: the counters scaled by what they read for a plain copy of known size); None for
@@ -276,6 +301,14 @@ def main():
     if not args.no_cpu:
         out["cpu_baseline"] = cpu_baseline(kw, args.config, L, args.cpu_budget)
     gpu.close()
+    # the plain-copy HBM rate at the streaming kernels' traffic sizes (measured after this library's context is
+    # closed): what a kernel that only moves these bytes reaches on this part
+    for key in ("prepass", "rot_q8"):
+        if key in out:
+            cr = copy_rates([out[key]["bytes"]])[0]
+            if cr:
+                out[key]["copy_GB/s"] = round(cr / 1e9, 1)
+                out[key]["frac_copy"] = round(out[key]["GB/s"] * 1e9 / cr, 4)
     print(json.dumps(out), flush=True)
 
 

@@ -213,6 +213,7 @@ void attention_wave_kernel(const char *__restrict__ Q, const char *__restrict__ 
       for (int i = 0; i < 16; i++) o[u][db][i] = 0.0f;
   // l: row sums up to the previous block; la: running partial row sums (four chains per query tile)
   float m[2] = {-INFINITY, -INFINITY}, l[2] = {0.0f, 0.0f};
+  float nmv[2] = {0.0f, 0.0f};  // -m (0 while m = -inf): the exponent offset, changed only where m changes
   float la[2][4] = {{0.0f, 0.0f, 0.0f, 0.0f}, {0.0f, 0.0f, 0.0f, 0.0f}};
   SAcc s[2][2];    // [key tile t][query tile u]
   i32x4 pb[2][2][2]; // [t][u][16-key step within t]: 8 packed 16-bit P values (whole dwords, so that the
@@ -382,7 +383,7 @@ void attention_wave_kernel(const char *__restrict__ Q, const char *__restrict__ 
   auto sub_tile = [&](Ops &op, int j, int t, int u, bool has_pv, bool has_next, bool mask, bool refresh, int jn,
                       int tn, float (&la)[4], int st0 = 0, int stn = 0, int sj = 0) {
     dump_scores(s[t][u], j, t, u, QK8 && SEEDED);
-    const float nm = m[u] == -INFINITY ? 0.0f : -m[u];
+    const float nm = nmv[u];
     float xv[16];
     int npv = 0, ns = 0;
     auto pv = [&]() {  // next P V MFMA of this sub-tile (the operand refresh also when there is none)
@@ -541,6 +542,7 @@ void attention_wave_kernel(const char *__restrict__ Q, const char *__restrict__ 
 #pragma unroll
           for (int i = 0; i < 16; i++) o[u][db][i] *= f;
         const float nm = mn == -INFINITY ? 0.0f : -mn;
+        nmv[u] = nm;
         tot[u] = l[u] + (exps(xs[0], qsc[u], nm, pb[0][u]) + exps(xs[1], qsc[u], nm, pb[1][u]));
         la[u][0] = tot[u];
         la[u][1] = la[u][2] = la[u][3] = 0.0f;
