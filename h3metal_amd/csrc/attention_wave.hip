@@ -82,7 +82,9 @@ struct CfgW {
   static constexpr int NCH = NP / 2;   // score MFMAs per 32x32 tile
   static constexpr int KBYTES = BK * RB, VBYTES = BK * D * 2;
   static constexpr int KOFF = 0, VOFF = NRV * KBYTES, SOFF = VOFF + NRV * VBYTES;
-  static constexpr int LDS = SOFF + (QK8 ? NRV * BK * 4 : 0);
+  // int8: key scales ks, then the seed corrections -SEED_F * ks (made in LDS once per block by the waves)
+  static constexpr int COFF = SOFF + (QK8 ? NRV * BK * 4 : 0);
+  static constexpr int LDS = COFF + (QK8 ? NRV * BK * 4 : 0);
   static constexpr int KDMA = KBYTES / (NWV * 1024);  // 16-byte LDS-direct loads per wave and block
   static constexpr int VDMA = VBYTES / (NWV * 1024);
 };
@@ -383,6 +385,14 @@ void attention_wave_kernel(const char *__restrict__ Q, const char *__restrict__ 
   auto sub_tile = [&](Ops &op, int j, int t, int u, bool has_pv, bool has_next, bool mask, bool refresh, int jn,
                       int tn, float (&la)[4], int st0 = 0, int stn = 0, int sj = 0) {
     dump_scores(s[t][u], j, t, u, QK8 && SEEDED);
+    if constexpr (QK8 && SEEDED) {
+      if (u == 0) {  // the seed corrections of this key tile, shared by both query tiles
+#pragma unroll
+        for (int g = 0; g < 4; g++)
+          op.c4[g] = *(const f32x4 *)((const float *)(smem + C::COFF) + (j % NRV) * BK + 32 * t + 16 * (g >> 1) +
+                                      8 * hl + 4 * (g & 1));
+      }
+    }
     const float nm = nmv[u];
     float xv[16];
     int npv = 0, ns = 0;
@@ -420,7 +430,6 @@ void attention_wave_kernel(const char *__restrict__ Q, const char *__restrict__ 
       }
     };
     auto mu = [&](int g) {  // int8: s * ks * 2^-26; keys past Lk to -inf
-      if (QK8 && SEEDED && u == 0) op.c4[g] = op.k4[g] * -SEED_F;
 #pragma unroll
       for (int e = 0; e < 4; e++) {
         const int i = 4 * g + e;
@@ -504,7 +513,12 @@ void attention_wave_kernel(const char *__restrict__ Q, const char *__restrict__ 
     else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
     tick(3);
+    // the scales of block j + 2 landed before this barrier: their seed corrections, published by the next one
+    // (every wave writes the same 64 values)
+    float kv = 0.0f;
+    if constexpr (QK8 && SEEDED) kv = ((const float *)(smem + C::SOFF))[((j + 2) % NRV) * BK + lane];
     sub_tile(op, j, 1, 1, has_pv, has_next, mask, true, j + 1, 0, la[1], 0, KS + (C::VDMA - VE0), j);
+    if constexpr (QK8 && SEEDED) ((float *)(smem + C::COFF))[((j + 2) % NRV) * BK + lane] = kv * -SEED_F;
     tick(4);
     tot[1] = (la[1][0] + la[1][1]) + (la[1][2] + la[1][3]);
     bad = bad | !(tot[1] - l[1] <= SUM_LIMIT);
@@ -561,6 +575,12 @@ void attention_wave_kernel(const char *__restrict__ Q, const char *__restrict__ 
     stage_v(0);
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
+    if constexpr (QK8 && SEEDED) {  // seed corrections of blocks 0 and 1
+#pragma unroll
+      for (int b2 = 0; b2 < 2; b2++)
+        ((float *)(smem + C::COFF))[b2 * BK + lane] = ((const float *)(smem + C::SOFF))[b2 * BK + lane] * -SEED_F;
+      __syncthreads();
+    }
     {
       i32x4 ka[C::NCH];
 #pragma unroll
