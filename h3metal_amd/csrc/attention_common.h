@@ -28,8 +28,11 @@ struct Split {
 // The wave-pipelined kernel (attention_wave.hip): launches it (and the merge of a tail split) for D = 128 without
 // a causal mask. qkt, vt, ot: T_I8 / T_BF16 / T_F16 / T_F32 codes; `dump` (the scores hook) also writes the raw
 // score accumulators to `dump` [H][Lq][L]. Returns 0, or -1 with a message.
-constexpr int WAVE_BQ = 256;       // query rows per workgroup of the wave-pipelined kernel (64 per wave)
-constexpr int WAVE_THREADS = 256;  // its workgroup: 4 waves, one per SIMD
+#ifndef WAVE_NU
+#define WAVE_NU 2
+#endif
+constexpr int WAVE_BQ = 128 * WAVE_NU;  // query rows per workgroup of the wave-pipelined kernel (32 WAVE_NU per wave)
+constexpr int WAVE_THREADS = 256;       // its workgroup: 4 waves, one per SIMD
 int launch_attention_wave(int qkt, int vt, int ot, bool dump, const Exec &ex, const Arg *args, const AttnParams &p,
                           int nqb, const Split &sp, std::string *err);
 

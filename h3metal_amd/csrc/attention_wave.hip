@@ -42,6 +42,11 @@ __device__ __forceinline__ void o_fence(f32x16 (&o)[2][4]) {
                : "+a"(o[0][0]), "+a"(o[0][1]), "+a"(o[0][2]), "+a"(o[0][3]), "+a"(o[1][0]), "+a"(o[1][1]),
                  "+a"(o[1][2]), "+a"(o[1][3]));
 }
+__device__ __forceinline__ void o_fence(f32x16 (&o)[3][4]) {
+  asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 4"
+               : "+a"(o[0][0]), "+a"(o[0][1]), "+a"(o[0][2]), "+a"(o[0][3]), "+a"(o[1][0]), "+a"(o[1][1]),
+                 "+a"(o[1][2]), "+a"(o[1][3]), "+a"(o[2][0]), "+a"(o[2][1]), "+a"(o[2][2]), "+a"(o[2][3]));
+}
 
 // First int8 score MFMA of a chain, accumulating onto the seed: the bits of 1/(2 pi) are an inline constant of
 // the srcC operand (no registers, no moves). Assembly, because the builtin materialises the constant vector in
@@ -54,8 +59,9 @@ __device__ __forceinline__ i32x16 mma_i8_seeded(i32x4 a, i32x4 b) {
 }
 
 constexpr int NWV = 4;              // waves per workgroup
-constexpr int BQV = WAVE_BQ;        // query rows per workgroup (64 per wave)
-static_assert(BQV == NWV * 64, "64 query rows per wave");
+constexpr int NU = WAVE_NU;         // 32-query MFMA tiles per wave (sharing every K and V operand read)
+constexpr int BQV = WAVE_BQ;        // query rows per workgroup
+static_assert(BQV == NWV * 32 * NU, "32 NU query rows per wave");
 constexpr int NRV = 4;              // ring depth (blocks)
 constexpr float SUM_LIMIT = 65536.0f;
 // int8 score accumulators start from the bits of the float 1/(2 pi) (an inline constant of the MFMA's C operand,
@@ -119,12 +125,12 @@ void attention_wave_kernel(const char *__restrict__ Q, const char *__restrict__ 
   const int h = lid / nqb, qb = lid - h * nqb;
   const int kvh = h / (p.H / p.KVH);
   // this lane's query rows: q0 + 32 u for the two query tiles u
-  const int q0 = qb * BQV + w * 64 + l32;
+  const int q0 = qb * BQV + w * (32 * NU) + l32;
 
   // Q operands (B of S^T = K Q^T), kept in registers: row q0 + 32 u, piece 2c + hl of each 32-byte chunk c
-  i32x4 qreg[2][C::NCH];
+  i32x4 qreg[NU][C::NCH];
 #pragma unroll
-  for (int u = 0; u < 2; u++) {
+  for (int u = 0; u < NU; u++) {
     const int q = q0 + 32 * u;
     const bool ok = q < p.Lq;
     const char *qrow = Q + ((size_t)h * p.q_rows + (ok ? q : 0)) * C::RB;
@@ -135,17 +141,17 @@ void attention_wave_kernel(const char *__restrict__ Q, const char *__restrict__ 
       asm volatile("" : "+a"(qreg[u][c]));  // from here on Q lives in AGPRs only
     }
   }
-  float qsc[2];
+  float qsc[NU];
 #pragma unroll
-  for (int u = 0; u < 2; u++) {
+  for (int u = 0; u < NU; u++) {
     const int q = q0 + 32 * u;
     qsc[u] = p.scale;
     if constexpr (QK8) qsc[u] = q < p.Lq ? fmaxf(qs[(size_t)h * p.q_rows + q] * p.scale, FLT_MIN) : 1.0f;
   }
   // the query scales of the main loop's seeded scores (s * ks * 2^-26)
-  float qsw[2];
+  float qsw[NU];
 #pragma unroll
-  for (int u = 0; u < 2; u++) qsw[u] = QK8 && SEEDED ? qsc[u] * SEED_SCALE : qsc[u];
+  for (int u = 0; u < NU; u++) qsw[u] = QK8 && SEEDED ? qsc[u] * SEED_SCALE : qsc[u];
 
   int key0 = 0, Lk = p.L;
   if (unit >= 0) {
@@ -206,24 +212,31 @@ void attention_wave_kernel(const char *__restrict__ Q, const char *__restrict__ 
       dma16(lds0 + C::VOFF + (blk % NRV) * C::VBYTES + (r * NWV + w) * 1024, vgo[r], rv);
   };
 
-  f32x16 o[2][D / 32];
+  f32x16 o[NU][D / 32];
 #pragma unroll
-  for (int u = 0; u < 2; u++)
+  for (int u = 0; u < NU; u++)
 #pragma unroll
     for (int db = 0; db < D / 32; db++)
 #pragma unroll
       for (int i = 0; i < 16; i++) o[u][db][i] = 0.0f;
   // l: row sums up to the previous block; la: running partial row sums (four chains per query tile)
-  float m[2] = {-INFINITY, -INFINITY}, l[2] = {0.0f, 0.0f};
-  float nmv[2] = {0.0f, 0.0f};  // -m (0 while m = -inf): the exponent offset, changed only where m changes
-  float la[2][4] = {{0.0f, 0.0f, 0.0f, 0.0f}, {0.0f, 0.0f, 0.0f, 0.0f}};
-  SAcc s[2][2];    // [key tile t][query tile u]
-  i32x4 pb[2][2][2]; // [t][u][16-key step within t]: 8 packed 16-bit P values (whole dwords, so that the
+  float m[NU], l[NU];
+  float nmv[NU];  // -m (0 while m = -inf): the exponent offset, changed only where m changes
+  float la[NU][4];  // running partial row sums (four chains per query tile)
+#pragma unroll
+  for (int u = 0; u < NU; u++) {
+    m[u] = -INFINITY;
+    l[u] = nmv[u] = 0.0f;
+#pragma unroll
+    for (int c = 0; c < 4; c++) la[u][c] = 0.0f;
+  }
+  SAcc s[2][NU];    // [key tile t][query tile u]
+  i32x4 pb[2][NU][2]; // [t][u][16-key step within t]: 8 packed 16-bit P values (whole dwords, so that the
                      // rare path's writes merge with the common path's as whole registers)
 #pragma unroll
   for (int t = 0; t < 2; t++)
 #pragma unroll
-    for (int u = 0; u < 2; u++) {
+    for (int u = 0; u < NU; u++) {
 #pragma unroll
       for (int i = 0; i < 16; i++) s[t][u][i] = 0;
 #pragma unroll
@@ -437,7 +450,7 @@ void attention_wave_kernel(const char *__restrict__ Q, const char *__restrict__ 
         else if constexpr (QK8) xv[i] *= op.k4[g][e];
         if (mask && j * BK + 32 * t + 16 * (i >> 3) + 8 * hl + (i & 7) >= Lk) xv[i] = -INFINITY;
       }
-      if (QK8 && refresh && u == 1) op.k4[g] = sread(jn, tn, g);
+      if (QK8 && refresh && u == NU - 1) op.k4[g] = sread(jn, tn, g);
     };
     auto fm = [&](int g) {
 #pragma unroll
@@ -496,19 +509,29 @@ void attention_wave_kernel(const char *__restrict__ Q, const char *__restrict__ 
     // (read up to step j - 1's recompute) and wait for this step's barrier.
     constexpr int KS = C::KDMA + (QK8 ? 1 : 0);  // K and scale loads come first in stage_one's order
     constexpr int VE0 = QK8 ? C::VDMA : 0;       // V loads issued before the barrier
-    sub_tile(op, j, 0, 0, has_pv, has_next, mask, false, 0, 0, la[0], KS, QK8 ? 2 : 0, j);
-    tick(0);
-    sub_tile(op, j, 0, 1, has_pv, has_next, mask, true, j, 1, la[1], KS + 2, QK8 ? 1 : 0, j);
-    tick(1);
-    sub_tile(op, j, 1, 0, has_pv, has_next, mask, false, 0, 0, la[0], KS + 3, QK8 ? 1 : 0, j);
-    tick(2);
-    // block j's row sums are the growth of the running partial sums; query tile 0's are complete here. A sum
-    // above SUM_LIMIT (or NaN) means a score far above the reference maximum: the block is recomputed below
-    float tot[2];
-    tot[0] = (la[0][0] + la[0][1]) + (la[0][2] + la[0][3]);
-    bool bad = !(tot[0] - l[0] <= SUM_LIMIT);
-    // this wave's loads of the previous step (this step's V loads, the newest, may still be in flight)
     static_assert(C::VDMA == 4, "V loads per wave and step");
+    // sub-tiles (t, u) in order; the barrier precedes the last one, (1, NU - 1). With int8 scores the V loads go
+    // 2, 1, 1 into the first three sub-tiles.
+    float tot[NU];
+    bool bad = false;
+    int st = KS;
+#pragma unroll
+    for (int idx = 0; idx < 2 * NU - 1; idx++) {
+      const int t = idx / NU, u = idx % NU;
+      const int n = QK8 ? (idx == 0 ? 2 : idx <= 2 ? 1 : 0) : 0;
+      const bool last_u = u == NU - 1;
+      sub_tile(op, j, t, u, has_pv, has_next, mask, last_u, t == 0 ? j : j + 1, t == 0 ? 1 : 0, la[u], st, n, j);
+      st += n;
+      tick(idx < 3 ? idx : 2);
+      if (t == 1) {
+        // block j's row sums are the growth of the running partial sums; query tile u's are complete here. A
+        // sum above SUM_LIMIT (or NaN) means a score far above the reference maximum: the block is recomputed
+        // below
+        tot[u] = (la[u][0] + la[u][1]) + (la[u][2] + la[u][3]);
+        bad = bad | !(tot[u] - l[u] <= SUM_LIMIT);
+      }
+    }
+    // this wave's loads of the previous step (this step's V loads, the newest, may still be in flight)
     if constexpr (QK8) asm volatile("s_waitcnt vmcnt(4)" ::: "memory");
     else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
@@ -517,11 +540,11 @@ void attention_wave_kernel(const char *__restrict__ Q, const char *__restrict__ 
     // (every wave writes the same 64 values)
     float kv = 0.0f;
     if constexpr (QK8 && SEEDED) kv = ((const float *)(smem + C::SOFF))[((j + 2) % NRV) * BK + lane];
-    sub_tile(op, j, 1, 1, has_pv, has_next, mask, true, j + 1, 0, la[1], 0, KS + (C::VDMA - VE0), j);
+    sub_tile(op, j, 1, NU - 1, has_pv, has_next, mask, true, j + 1, 0, la[NU - 1], 0, KS + (C::VDMA - VE0), j);
     if constexpr (QK8 && SEEDED) ((float *)(smem + C::COFF))[((j + 2) % NRV) * BK + lane] = kv * -SEED_F;
     tick(4);
-    tot[1] = (la[1][0] + la[1][1]) + (la[1][2] + la[1][3]);
-    bad = bad | !(tot[1] - l[1] <= SUM_LIMIT);
+    tot[NU - 1] = (la[NU - 1][0] + la[NU - 1][1]) + (la[NU - 1][2] + la[NU - 1][3]);
+    bad = bad | !(tot[NU - 1] - l[NU - 1] <= SUM_LIMIT);
 #ifdef WAVE_NO_CHECK
     bad = false;
 #endif
@@ -530,7 +553,7 @@ void attention_wave_kernel(const char *__restrict__ Q, const char *__restrict__ 
     if (__builtin_expect(j == 0 || __builtin_amdgcn_ballot_w64(bad) != 0, 0)) {
       o_fence(o);  // P V MFMAs of this step may still be writing O
 #pragma unroll
-      for (int u = 0; u < 2; u++) {
+      for (int u = 0; u < NU; u++) {
         // block j's scores of query tile u again (K and scales are still in their ring slots)
         f32x16 xs[2];
         float bmax = -INFINITY;
@@ -563,8 +586,8 @@ void attention_wave_kernel(const char *__restrict__ Q, const char *__restrict__ 
       }
       asm volatile("s_nop 2" ::: "memory");  // VALU writes of O before the next MFMA reads it
     }
-    l[0] = tot[0];
-    l[1] = tot[1];
+#pragma unroll
+    for (int u = 0; u < NU; u++) l[u] = tot[u];
     tick(5);
   };
 
@@ -587,7 +610,7 @@ void attention_wave_kernel(const char *__restrict__ Q, const char *__restrict__ 
       for (int t = 0; t < 2; t++) {
         kops(0, t, ka);
 #pragma unroll
-        for (int u = 0; u < 2; u++) score_mfmas(s[t][u], ka, u, QK8 && SEEDED);
+        for (int u = 0; u < NU; u++) score_mfmas(s[t][u], ka, u, QK8 && SEEDED);
       }
     }
     Ops op;
@@ -605,7 +628,7 @@ void attention_wave_kernel(const char *__restrict__ Q, const char *__restrict__ 
         for (int k = 0; k < 8; k++) op.va[k] = vread(nblk - 1, 1, k);
       }
 #pragma unroll
-      for (int u = 0; u < 2; u++)
+      for (int u = 0; u < NU; u++)
 #pragma unroll
         for (int k = 0; k < 8; k++) mma_pv_acc<VT>(o[u][k & 3], op.va[k], __builtin_bit_cast(VT8, pb[t][u][k >> 2]));
     }
@@ -623,7 +646,7 @@ void attention_wave_kernel(const char *__restrict__ Q, const char *__restrict__ 
   return;
 #endif
 #pragma unroll
-  for (int u = 0; u < 2; u++) {
+  for (int u = 0; u < NU; u++) {
     const int q = q0 + 32 * u;
     const float lt = l[u] + __shfl_xor(l[u], 32);
     if (unit >= 0) {
