@@ -492,7 +492,7 @@ void attention_wave_kernel(const char *__restrict__ Q, const char *__restrict__ 
   // recompute; V(j + 1) replaces V(j - 3); scales(j + 3) replace scales(j - 1).
 #ifdef WAVE_TIMING
   // timing-only builds: shader-clock ticks per phase of the step, written to the scores buffer at the end
-  unsigned long long tph[6] = {0, 0, 0, 0, 0, 0}, tlast = 0;
+  unsigned long long tph[7] = {0, 0, 0, 0, 0, 0, 0}, tlast = 0;
   auto tick = [&](int k) {
     const unsigned long long now = __builtin_amdgcn_s_memtime();
     if (k >= 0) tph[k] += now - tlast;
@@ -534,6 +534,7 @@ void attention_wave_kernel(const char *__restrict__ Q, const char *__restrict__ 
     // this wave's loads of the previous step (this step's V loads, the newest, may still be in flight)
     if constexpr (QK8) asm volatile("s_waitcnt vmcnt(4)" ::: "memory");
     else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    tick(6);
     __syncthreads();
     tick(3);
     // the scales of block j + 2 landed before this barrier: their seed corrections, published by the next one
@@ -640,8 +641,8 @@ void attention_wave_kernel(const char *__restrict__ Q, const char *__restrict__ 
   // the output's first bytes carry the ticks (workgroup b, wave w at 64 (NWV b + w)); no output is written
   if (lane == 0) {
     long long *tp = (long long *)O + ((size_t)blockIdx.x * NWV + w) * 8;
-    for (int k = 0; k < 6; k++) tp[k] = (long long)tph[k];
-    tp[6] = nblk;
+    for (int k = 0; k < 7; k++) tp[k] = (long long)tph[k];
+    tp[7] = nblk;
   }
   return;
 #endif
