@@ -900,6 +900,12 @@ int launch_attention(const Pipeline &pl, const Exec &ex, const Arg *args, int na
   // the wave-pipelined kernel: D = 128 without a causal mask (unless GROUPS selects an older kernel)
   constexpr bool CANW = !CAUSAL && D == 128;
   const bool usew = CANW && pl.ival[2];
+  // the wave kernel addresses a head's K/V rows (and the blocks its pipeline stages past the end) with 32-bit
+  // byte offsets
+  if (usew && (uint64_t)(p.L + 4 * BK) * D * 2 > 0xffffffffull) {
+    *err = "L = " + std::to_string(p.L) + " keys: too long for 32-bit K/V row offsets";
+    return -1;
+  }
   if (DUMP) {
     if (nargs < 8 || !args[7].ptr) {
       *err = "the scores hook needs its scores buffer at index 7";
@@ -943,7 +949,8 @@ int launch_attention(const Pipeline &pl, const Exec &ex, const Arg *args, int na
   }
   // Tail split (not for causal masks, whose tiles differ in length, nor for the scores dump): the R tiles of a
   // last, partly filled round of CUs become R * s key chunks, s <= CUs / R, each at least 2 key blocks.
-  Split sp{(int)ntiles, 0, 0, nullptr};
+  Split sp{(int)ntiles, 0, 0, nullptr, 0};
+  if (usew) sp.rnd = cu_count() / 8;  // the wave kernel alternates its key order between rounds of an XCD
   const int cus = pl.ival[0] ? cu_count() : 0;
   const int kblocks = (p.L + BK - 1) / BK;
   if (!CAUSAL && (!DUMP || usew) && cus > 0) {

@@ -23,6 +23,7 @@ struct Split {
   int s;      // chunks per split tile (0: no split)
   int cb;     // key blocks per chunk
   float *ws;  // partial states: [unit][BQ rows][DG + 4]
+  int rnd;    // compute units per XCD (workgroups per XCD and round; 0: unknown)
 };
 
 // The wave-pipelined kernel (attention_wave.hip): launches it (and the merge of a tail split) for D = 128 without

@@ -114,10 +114,16 @@ void attention_wave_kernel(const char *__restrict__ Q, const char *__restrict__ 
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int b = blockIdx.x;
   int lid, unit = -1;
+  bool rev = false;
   if (b < sp.nfull) {
     const int nb = sp.nfull;
     const int per = nb >> 3, rem = nb & 7, xcd = b & 7, loc = b >> 3;
     lid = (xcd < rem ? xcd * (per + 1) : rem * (per + 1) + (xcd - rem) * per) + loc;
+#ifndef WAVE_NO_REV
+    // Every other round of an XCD's workgroups (one per CU) takes the key blocks in the order L-2, ..., 0, L-1:
+    // it starts on the blocks the round before it read last, still in the XCD's L2 (a head's K and V outgrow it)
+    rev = sp.rnd > 0 && ((loc / sp.rnd) & 1);
+#endif
   } else {
     unit = b - sp.nfull;
     lid = sp.nfull + unit / sp.s;
@@ -162,15 +168,19 @@ void attention_wave_kernel(const char *__restrict__ Q, const char *__restrict__ 
   const char *Vh = V + ((size_t)kvh * p.k_rows + key0) * D * 2;
   const float *ksh = QK8 ? ks + (size_t)kvh * p.k_rows + key0 : nullptr;
   const int nblk = Lk > 0 ? (Lk + BK - 1) / BK : 0;
+  // the key block that step j works on; the partial block (if any) stays last, blocks past the end stay there
+  auto kblk = [&](int j) { return __builtin_amdgcn_readfirstlane(rev && j < nblk - 1 ? nblk - 2 - j : j); };
 
   // -- LDS-direct staging. Load instruction r of this wave writes 1 KB at LDS (r * NWV + w) * 1024 of the block's
-  // ring slot; each lane fetches the 16-byte piece whose swizzled position that is. Rows at or past Lk read as
-  // zero (descriptor range).
-  auto rsrc = [&](const void *base, int blk, int row_bytes) {
-    const int rows = max(0, Lk - blk * BK);
-    return __builtin_amdgcn_make_buffer_rsrc((void *)((const char *)base + (size_t)blk * BK * row_bytes), (short)0,
-                                             __builtin_amdgcn_readfirstlane(rows * row_bytes), 0x00020000);
+  // ring slot; each lane fetches the 16-byte piece whose swizzled position that is. One descriptor per array
+  // covers this workgroup's Lk rows; the block's offset goes into the lane's VGPR offset (the part of the
+  // address the range check covers), so rows at or past Lk, and blocks past the end, read as zero.
+  auto rsrc = [&](const void *base, int row_bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc((void *)base, (short)0,
+                                             __builtin_amdgcn_readfirstlane(max(0, Lk) * row_bytes), 0x00020000);
   };
+  const __amdgpu_buffer_rsrc_t rk = rsrc(Kh, C::RB), rv = rsrc(Vh, D * 2);
+  const __amdgpu_buffer_rsrc_t rs = QK8 ? rsrc(ksh, 4) : rk;
   unsigned kgo[C::KDMA], vgo[C::VDMA];
 #pragma unroll
   for (int r = 0; r < C::KDMA; r++) {
@@ -186,30 +196,32 @@ void attention_wave_kernel(const char *__restrict__ Q, const char *__restrict__ 
   }
   auto stage_k = [&](int blk) {  // K and key scales of block blk
     const int slot = blk % NRV;
-    const __amdgpu_buffer_rsrc_t rk = rsrc(Kh, blk, C::RB);
+    const unsigned kb0 = (unsigned)kblk(blk) * (BK * C::RB);
 #pragma unroll
-    for (int r = 0; r < C::KDMA; r++) dma16(lds0 + C::KOFF + slot * C::KBYTES + (r * NWV + w) * 1024, kgo[r], rk);
+    for (int r = 0; r < C::KDMA; r++) dma16(lds0 + C::KOFF + slot * C::KBYTES + (r * NWV + w) * 1024, kgo[r] + kb0, rk);
     // every wave loads the block's 64 scales to the same place (no wave-dependent branch or wait count)
-    if constexpr (QK8) dma4(lds0 + C::SOFF + slot * BK * 4, lane * 4, rsrc(ksh, blk, 4));
+    if constexpr (QK8) dma4(lds0 + C::SOFF + slot * BK * 4, lane * 4 + (unsigned)kblk(blk) * (BK * 4), rs);
   };
   // the same loads one at a time (K and scales of block kb, V of block vb), so that they can be spread between
   // MFMAs: load i < KDMA is a K piece, then (int8) the scales, then the V pieces
   constexpr int NLOADS = C::KDMA + (QK8 ? 1 : 0) + C::VDMA;
   auto stage_one = [&](int i, int kb, int vb) {
     if (i < C::KDMA) {
-      dma16(lds0 + C::KOFF + (kb % NRV) * C::KBYTES + (i * NWV + w) * 1024, kgo[i], rsrc(Kh, kb, C::RB));
+      dma16(lds0 + C::KOFF + (kb % NRV) * C::KBYTES + (i * NWV + w) * 1024,
+            kgo[i] + (unsigned)kblk(kb) * (BK * C::RB), rk);
     } else if (QK8 && i == C::KDMA) {
-      dma4(lds0 + C::SOFF + (kb % NRV) * BK * 4, lane * 4, rsrc(ksh, kb, 4));
+      dma4(lds0 + C::SOFF + (kb % NRV) * BK * 4, lane * 4 + (unsigned)kblk(kb) * (BK * 4), rs);
     } else {
       const int r = i - C::KDMA - (QK8 ? 1 : 0);
-      dma16(lds0 + C::VOFF + (vb % NRV) * C::VBYTES + (r * NWV + w) * 1024, vgo[r], rsrc(Vh, vb, D * 2));
+      dma16(lds0 + C::VOFF + (vb % NRV) * C::VBYTES + (r * NWV + w) * 1024,
+            vgo[r] + (unsigned)kblk(vb) * (BK * D * 2), rv);
     }
   };
   auto stage_v = [&](int blk) {
-    const __amdgpu_buffer_rsrc_t rv = rsrc(Vh, blk, D * 2);
+    const unsigned vb0 = (unsigned)kblk(blk) * (BK * D * 2);
 #pragma unroll
     for (int r = 0; r < C::VDMA; r++)
-      dma16(lds0 + C::VOFF + (blk % NRV) * C::VBYTES + (r * NWV + w) * 1024, vgo[r], rv);
+      dma16(lds0 + C::VOFF + (blk % NRV) * C::VBYTES + (r * NWV + w) * 1024, vgo[r] + vb0, rv);
   };
 
   f32x16 o[NU][D / 32];
@@ -317,7 +329,7 @@ void attention_wave_kernel(const char *__restrict__ Q, const char *__restrict__ 
     if (mask) {
 #pragma unroll
       for (int i = 0; i < 16; i++)
-        if (j * BK + 32 * t + 16 * (i >> 3) + 8 * hl + (i & 7) >= Lk) x[i] = -INFINITY;
+        if (kblk(j) * BK + 32 * t + 16 * (i >> 3) + 8 * hl + (i & 7) >= Lk) x[i] = -INFINITY;
     }
     return x;
   };
@@ -345,7 +357,7 @@ void attention_wave_kernel(const char *__restrict__ Q, const char *__restrict__ 
                             __builtin_shufflevector(a, a, 8, 9, 10, 11), __builtin_shufflevector(a, a, 12, 13, 14, 15)};
 #pragma unroll
         for (int r = 0; r < 4; r++) {
-          const int key = key0 + j * BK + 32 * t + 16 * (r >> 1) + 8 * hl + 4 * (r & 1);
+          const int key = key0 + kblk(j) * BK + 32 * t + 16 * (r >> 1) + 8 * hl + 4 * (r & 1);
           int *dst = dump + ((size_t)h * p.Lq + q) * p.L + key;
           if (key + 4 <= key0 + Lk && (p.L & 3) == 0) {
             *(i32x4 *)dst = g[r];
@@ -448,7 +460,7 @@ void attention_wave_kernel(const char *__restrict__ Q, const char *__restrict__ 
         const int i = 4 * g + e;
         if constexpr (QK8 && SEEDED) xv[i] = fmaf(xv[i], op.k4[g][e], op.c4[g][e]);
         else if constexpr (QK8) xv[i] *= op.k4[g][e];
-        if (mask && j * BK + 32 * t + 16 * (i >> 3) + 8 * hl + (i & 7) >= Lk) xv[i] = -INFINITY;
+        if (mask && kblk(j) * BK + 32 * t + 16 * (i >> 3) + 8 * hl + (i & 7) >= Lk) xv[i] = -INFINITY;
       }
       if (QK8 && refresh && u == NU - 1) op.k4[g] = sread(jn, tn, g);
     };
