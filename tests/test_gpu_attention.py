@@ -323,6 +323,41 @@ def test_config4_int32_scores_and_output_at_full_key_length(gpu):
     assert err.max() < NS_MAX and err.mean() < NS_MEAN, (err.max(), err.mean())
 
 
+def test_int32_scores_and_output_in_reversed_rounds(gpu):
+    """Enough workgroups that every other round of an XCD's workgroups takes its key blocks in the order
+    L-2, ..., 0, L-1 (520 one-tile heads: the rounds after the first 256 workgroups run reversed), with a ragged
+    last block (L = 300: 5 blocks, the last with 44 keys) and GQA (8 key/value heads): the int32 scores of every
+    head bit-exact against exact integer products (the scores hook writes each at its key index, so a block
+    mapped to the wrong keys fails), and the output of sampled heads against float64 attention."""
+    rng = np.random.default_rng(45)
+    H, KVH, D, Lq, L = 520, 8, 128, 256, 300
+    qi = rng.integers(-127, 128, (H, Lq, D)).astype(np.int8)
+    ki = rng.integers(-127, 128, (KVH, L, D)).astype(np.int8)
+    qsc = rng.uniform(1e-3, 2e-3, (H, Lq)).astype(np.float32)
+    ksc = rng.uniform(1e-3, 2e-3, (KVH, L)).astype(np.float32)
+    vb = to_bf16(rng.standard_normal((KVH, L, D)).astype(np.float32))
+    Q, K, V = gpu.upload(qi, "i8"), gpu.upload(ki, "i8"), gpu.upload(vb, "bf16")
+    qs, ks = gpu.upload(qsc), gpu.upload(ksc)
+    S = gpu.empty((H, Lq, L), "i32")
+    O = gpu.empty((Lq, H * D), "bf16")
+    print(f"[scores] reversed rounds H={H} KVH={KVH} Lq={Lq} L={L}", flush=True)
+    ops.attention_scores(gpu, Q, K, V, S, Lq=Lq, L=L, H=H, KVH=KVH, D=D, q_rows=Lq, k_rows=L, q_scale=qs,
+                         k_scale=ks, out=O, scale=D ** -0.5)
+    gpu.wait()
+    g = H // KVH
+    kf = ki.astype(np.float64)
+    want = np.einsum("hqd,hkd->hqk", qi.astype(np.float64), np.repeat(kf, g, axis=0), optimize=True)
+    got = S.numpy()
+    assert np.array_equal(got, want.astype(np.int32)), f"{(got != want).sum()} int32 scores differ"
+    heads = [0, 31, 32, 63, 100, 300, 519]
+    kd = ki * ksc[..., None].astype(np.float64)
+    ref = oa.ref_attention(qi[heads] * qsc[heads][..., None].astype(np.float64), kd[[h // g for h in heads]],
+                           from_bf16(vb)[[h // g for h in heads]], D ** -0.5)
+    out = from_bf16(O.numpy()).astype(np.float64).reshape(Lq, H, D)[:, heads].reshape(Lq, len(heads) * D)
+    err = np.abs(out - ref)
+    assert err.max() < NS_MAX and err.mean() < NS_MEAN, (err.max(), err.mean())
+
+
 def test_config4_int8_rotated_full_size(gpu):
     """Config 4 at full size: H=32, D=128, S=16896, outlier channels x20, rotation + int8 pre-pass, int8
     attention with bf16 V. On a seeded sample of query rows:
