@@ -41,6 +41,8 @@ enum { A_I8 = 0, A_F16 = 1, A_BF16 = 2 };
 // epilogue scaling: sa[m] * sw[n] (q8), sw[n] (h8), none (f16, bf16)
 enum { S_ROW_COL = 0, S_COL = 1, S_NONE = 2 };
 
+enum { T_BF16 = 1, T_F16 = 2, T_F32 = 3 };
+
 template <int AT>
 using AccOf = typename std::conditional<AT == A_I8, i32x16, f32x16>::type;
 
@@ -56,18 +58,28 @@ __device__ __forceinline__ AccOf<AT> mma(i32x4 a, i32x4 b, AccOf<AT> c) {
                                                    0, 0, 0);
 }
 
-enum { T_BF16 = 1, T_F16 = 2, T_F32 = 3 };
-
-constexpr int TM = 256, TN = 256, KS = 64;       // tile rows, columns, K bytes per step
+constexpr int KS = 64;                           // K bytes per step
 constexpr int NWG = 8;                           // waves per workgroup
 constexpr int WGN = 2, WGM = NWG / WGN;          // waves along the columns and the rows of the tile
-constexpr int WTM = TM / WGM, WTN = TN / WGN;    // wave tile
-constexpr int MI = WTM / 32, NJ = WTN / 32;      // 32 x 32 MFMA tiles per wave
-constexpr int NQA = TM / NWG / 16, NQW = TN / NWG / 16;  // 16-row LDS-direct loads per wave and step
-constexpr int LPS = NQA + NQW;                   // loads per wave and step
 constexpr int SW = 4;                            // row tiles per band of the tile order
 constexpr int NST = 4;                           // LDS stages
-constexpr int STAGE = (TM + TN) * KS;            // LDS bytes per stage
+// Tile configurations: 256 x 256 (the main grid) and 128 x 128 (the rows of a last, mostly empty round of
+// tiles, run as a second launch of their own)
+template <int TM_, int TN_>
+struct GTile {
+  static constexpr int TM = TM_, TN = TN_;                       // tile rows, columns
+  static constexpr int WTM = TM / WGM, WTN = TN / WGN;           // wave tile
+  static constexpr int MI = WTM / 32, NJ = WTN / 32;             // 32 x 32 MFMA tiles per wave
+  static constexpr int NQA = TM / NWG / 16, NQW = TN / NWG / 16;  // 16-row LDS-direct loads per wave and step
+  static constexpr int LPS = NQA + NQW;                          // loads per wave and step
+  static constexpr int STAGE = (TM + TN) * KS;                   // LDS bytes per stage
+  template <int OT>
+  static constexpr int lds_bytes() {
+    return std::max(NST * STAGE, OT == T_F32 ? TM / 2 * (TN * 4 + 16) : TM * (TN * 2 + 16));
+  }
+};
+using TileBig = GTile<256, 256>;
+using TileSmall = GTile<128, 128>;
 
 // 16-byte piece p of LDS row r (64 bytes) sits at slot p ^ ((r / 4) % 4)
 __device__ __forceinline__ int swz(int row, int piece) { return row * KS + ((piece ^ ((row >> 2) & 3)) << 4); }
@@ -80,7 +92,7 @@ __device__ __forceinline__ void store_out(char *p, float v) {
   else *(_Float16 *)p = (_Float16)v;
 }
 
-template <int OT, int EPI, bool HAS_BIAS, int AT, int SM>
+template <int OT, int EPI, bool HAS_BIAS, int AT, int SM, class TL>
 __global__ __launch_bounds__(NWG * 64) __attribute__((amdgpu_waves_per_eu(2))) void gemm_kernel(const char *__restrict__ A,
                                                            const char *__restrict__ W,
                                                            const float *__restrict__ sw, const float *__restrict__ sa,
@@ -88,6 +100,8 @@ __global__ __launch_bounds__(NWG * 64) __attribute__((amdgpu_waves_per_eu(2))) v
                                                            const unsigned char *__restrict__ rtype,
                                                            const float *__restrict__ gate, GemmParams p, int ntm,
                                                            int ntn, int ntypes, bool vec) {
+  constexpr int TM = TL::TM, TN = TL::TN, WTM = TL::WTM, WTN = TL::WTN, MI = TL::MI, NJ = TL::NJ;
+  constexpr int NQA = TL::NQA, NQW = TL::NQW, LPS = TL::LPS, STAGE = TL::STAGE;
   extern __shared__ __attribute__((aligned(16))) char smem[];
   const int tid = threadIdx.x, lane = tid & 63, hl = lane >> 5, l32 = lane & 31;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -175,12 +189,14 @@ __global__ __launch_bounds__(NWG * 64) __attribute__((amdgpu_waves_per_eu(2))) v
         for (int j = 0; j < NJ; j++)
           acc[i][j] = TR ? mma<AT>(cur.w[c][j], cur.a[c][i], acc[i][j]) : mma<AT>(cur.a[c][i], cur.w[c][j], acc[i][j]);
     constexpr int NR = 2 * (MI + NJ), NF = 2 * MI * NJ;  // LDS reads and MFMAs of a step
+    if constexpr (NF >= NR) {
 #pragma unroll
-    for (int g = 0; g < NR; g++) {
-      __builtin_amdgcn_sched_group_barrier(0x008, NF / NR, 0);  // MFMAs
-      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);        // one LDS read
+      for (int g = 0; g < NR; g++) {
+        __builtin_amdgcn_sched_group_barrier(0x008, NF / NR, 0);  // MFMAs
+        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);        // one LDS read
+      }
+      __builtin_amdgcn_sched_group_barrier(0x008, NF - NR * (NF / NR), 0);
     }
-    __builtin_amdgcn_sched_group_barrier(0x008, NF - NR * (NF / NR), 0);
   };
 
 #pragma unroll
@@ -459,24 +475,52 @@ int launch_gemm(const Pipeline &pl, const Exec &ex, const Arg *a, int nargs, con
   const bool vec = al16(a[4].ptr) && (p.c_stride * OSZ) % 16 == 0 && p.N % VE == 0 &&
                    (SM == S_NONE || al16(a[2].ptr)) && (!HAS_BIAS || al16(a[5].ptr)) &&
                    (!EPI || (al16(a[7].ptr) && p.g_stride % 4 == 0));
-  const int ntm = (p.M + TM - 1) / TM, ntn = (p.N + TN - 1) / TN;
-  auto kern = gemm_kernel<OT, EPI, HAS_BIAS, AT, SM>;
-  constexpr int LDS_BYTES =
-      std::max(NST * STAGE, OT == T_F32 ? TM / 2 * (TN * 4 + 16) : TM * (TN * 2 + 16));
-  static bool attr_set = false;
-  if (!attr_set) {
-    hipError_t e = hipFuncSetAttribute((const void *)kern, hipFuncAttributeMaxDynamicSharedMemorySize, LDS_BYTES);
-    if (e != hipSuccess) {
-      *err = std::string("hipFuncSetAttribute: ") + hipGetErrorString(e);
-      return -1;
+  // One grid of 256 x 256 tiles; when its last round of tiles would leave more than half the CUs idle, the
+  // trailing rows of tiles go to a second launch of 128 x 128 tiles (the same kernel on the sub-problem of those
+  // rows: A, sa, rtype and the output offset by the first row), if that shortens the estimated time (a small
+  // tile taken as 0.45 of a big one's time).
+  auto launch = [&](auto tl, int row0, int rows) -> int {
+    using TL = decltype(tl);
+    auto kern = gemm_kernel<OT, EPI, HAS_BIAS, AT, SM, TL>;
+    constexpr int LDS_BYTES = TL::template lds_bytes<OT>();
+    static bool attr_set = false;  // one per tile configuration
+    if (!attr_set) {
+      hipError_t e = hipFuncSetAttribute((const void *)kern, hipFuncAttributeMaxDynamicSharedMemorySize, LDS_BYTES);
+      if (e != hipSuccess) {
+        *err = std::string("hipFuncSetAttribute: ") + hipGetErrorString(e);
+        return -1;
+      }
+      attr_set = true;
     }
-    attr_set = true;
+    GemmParams q = p;
+    q.M = rows;
+    const int ntm = (rows + TL::TM - 1) / TL::TM, ntn = (p.N + TL::TN - 1) / TL::TN;
+    const size_t r0 = (size_t)row0;
+    hipLaunchKernelGGL(kern, dim3((unsigned)(ntm * ntn)), dim3(NWG * 64), LDS_BYTES, ex.stream,
+                       (const char *)a[0].ptr + r0 * p.a_stride * ES, (const char *)wptr,
+                       SM != S_NONE ? (const float *)a[2].ptr : nullptr,
+                       SM == S_ROW_COL ? (const float *)a[3].ptr + r0 : nullptr, a[4].ptr + r0 * p.c_stride * OSZ,
+                       HAS_BIAS ? (const float *)a[5].ptr : nullptr,
+                       EPI ? (const unsigned char *)a[6].ptr + r0 : nullptr, EPI ? (const float *)a[7].ptr : nullptr,
+                       q, ntm, ntn, ntypes, vec);
+    return 0;
+  };
+  constexpr int BT = TileBig::TM, ST = TileSmall::TM;
+  const int ntm = (p.M + BT - 1) / BT, ntn = (p.N + TileBig::TN - 1) / TileBig::TN;
+  const int cus = cu_count();
+  int main_rows = p.M;
+  if (cus > 0) {
+    const long nt = (long)ntm * ntn, R = nt % cus;
+    const int tr = (int)((R + ntn - 1) / ntn);  // trailing rows of tiles that hold the last round's tiles
+    if (R > 0 && 2 * R <= cus && tr < ntm) {
+      const int mrows = (ntm - tr) * BT;
+      const long small = (long)((p.M - mrows + ST - 1) / ST) * ((p.N + ST - 1) / ST);
+      const double t_split = (double)(((long)(ntm - tr) * ntn + cus - 1) / cus) + 0.45 * ((small + cus - 1) / cus);
+      if (t_split < (double)((nt + cus - 1) / cus)) main_rows = mrows;
+    }
   }
-  hipLaunchKernelGGL(kern, dim3((unsigned)(ntm * ntn)), dim3(NWG * 64), LDS_BYTES, ex.stream, (const char *)a[0].ptr,
-                     (const char *)wptr, SM != S_NONE ? (const float *)a[2].ptr : nullptr,
-                     SM == S_ROW_COL ? (const float *)a[3].ptr : nullptr, a[4].ptr,
-                     HAS_BIAS ? (const float *)a[5].ptr : nullptr, EPI ? (const unsigned char *)a[6].ptr : nullptr,
-                     EPI ? (const float *)a[7].ptr : nullptr, p, ntm, ntn, ntypes, vec);
+  if (launch(TileBig{}, 0, main_rows)) return -1;
+  if (main_rows < p.M && launch(TileSmall{}, main_rows, p.M - main_rows)) return -1;
   return 0;
 }
 

@@ -175,6 +175,60 @@ def test_config4_projection_shapes_sampled(gpu):
     assert np.array_equal(got[rows], to_bf16(v))
 
 
+@pytest.mark.parametrize("mode", ["f32", "bf16", "epi1"])
+def test_last_round_rows_on_small_tiles(gpu, mode):
+    """260 tiles of 256 x 256 on 256 CUs: the last row of tiles (rows 16384..16447) runs as a second launch of
+    128 x 128 tiles on the sub-problem of those rows; every row bit for bit (f32, the residual form) or equal to
+    the rounded oracle (bf16), the rows of both launches alike."""
+    rng = np.random.default_rng(46)
+    M, N, K = 16448, 1024, 128
+    a, sa, q, sw, b = make(rng, M, N, K, bias=True)
+    v = og.epilogue(og.int_product(a, q), sa, sw, b)
+    if mode == "epi1":
+        x0 = rng.standard_normal((M, N)).astype(np.float32)
+        types = rng.integers(0, 3, size=M).astype(np.uint8)
+        gates = rng.standard_normal((3, N)).astype(np.float32)
+        wt = ops.QWeight("q8", gpu.upload(q), gpu.upload(sw), N, K, bias=gpu.upload(b))
+        X = gpu.upload(x0)
+        print(f"[gemm] tail rows M={M} N={N} K={K} epi=1", flush=True)
+        ops.gemm(gpu, gpu.upload(a), wt, X, M, sa=gpu.upload(sa), epi=1, rtype=gpu.upload(types),
+                 gate=gpu.upload(gates), tile=(64, 256, 8))
+        gpu.wait()
+        want = og.residual(x0, v, gates, types)
+        assert np.array_equal(X.numpy().view(np.uint32), want.view(np.uint32))
+        return
+    got = run(gpu, a, sa, q, sw, b, M, out_dtype=mode)
+    if mode == "f32":
+        assert np.array_equal(got.view(np.uint32), v.view(np.uint32))
+    else:
+        assert np.array_equal(got, to_bf16(v))
+
+
+def test_config4_output_projection_sampled(gpu):
+    """The output projection of a config-4 block (M = 16896, N = K = 4096) into the float residual: 1056 tiles,
+    of which the last two rows of tiles run on 128 x 128 tiles; 48 sampled rows of each part bit for bit."""
+    rng = np.random.default_rng(47)
+    M, N, K = 16896, 4096, 4096
+    a = rng.integers(-127, 128, size=(M, K), dtype=np.int8)
+    sa = rng.uniform(0.001, 0.01, size=M).astype(np.float32)
+    q = rng.integers(-127, 128, size=(N, K), dtype=np.int8)
+    sw = rng.uniform(0.001, 0.01, size=N).astype(np.float32)
+    b = rng.standard_normal(N).astype(np.float32)
+    x0 = rng.standard_normal((M, N)).astype(np.float32)
+    types = rng.integers(0, 3, size=M).astype(np.uint8)
+    gates = rng.standard_normal((3, N)).astype(np.float32)
+    wt = ops.QWeight("q8", gpu.upload(q), gpu.upload(sw), N, K, bias=gpu.upload(b))
+    X = gpu.upload(x0)
+    print(f"[gemm] output projection M={M} N={N} K={K} epi=1", flush=True)
+    ops.gemm(gpu, gpu.upload(a), wt, X, M, sa=gpu.upload(sa), epi=1, rtype=gpu.upload(types),
+             gate=gpu.upload(gates), tile=(64, 256, 8))
+    gpu.wait()
+    rows = np.sort(np.concatenate([rng.choice(16384, 48, replace=False), 16384 + rng.choice(512, 48, replace=False)]))
+    v = og.epilogue(og.int_product(a[rows], q), sa[rows], sw, b)
+    want = og.residual(x0[rows], v, gates, types[rows])
+    assert np.array_equal(X.numpy()[rows].view(np.uint32), want.view(np.uint32))
+
+
 def test_refusals(gpu):
     rng = np.random.default_rng(44)
     a, sa, q, sw, _ = make(rng, 64, 256, 256)
