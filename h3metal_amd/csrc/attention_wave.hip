@@ -177,7 +177,8 @@ void attention_wave_kernel(const char *__restrict__ Q, const char *__restrict__ 
   // address the range check covers), so rows at or past Lk, and blocks past the end, read as zero.
   auto rsrc = [&](const void *base, int row_bytes) {
     return __builtin_amdgcn_make_buffer_rsrc((void *)base, (short)0,
-                                             __builtin_amdgcn_readfirstlane(max(0, Lk) * row_bytes), 0x00020000);
+                                             __builtin_amdgcn_readfirstlane((int)((unsigned)max(0, Lk) * (unsigned)row_bytes)),
+                                             0x00020000);
   };
   const __amdgpu_buffer_rsrc_t rk = rsrc(Kh, C::RB), rv = rsrc(Vh, D * 2);
   const __amdgpu_buffer_rsrc_t rs = QK8 ? rsrc(ksh, 4) : rk;
