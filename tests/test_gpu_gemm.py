@@ -229,6 +229,43 @@ def test_config4_output_projection_sampled(gpu):
     assert np.array_equal(X.numpy()[rows].view(np.uint32), want.view(np.uint32))
 
 
+@pytest.mark.parametrize("seed", range(16))
+def test_random_shape_sweep_bit_exact(gpu, seed):
+    """A seeded sweep of shapes (M up to 9000 rows, so that some grids pass 256 tiles and take the small-tile
+    tail launch; ragged N; K a multiple of 64), both epilogues, three output types, with and without bias:
+    f32 and the residual form bit for bit, 16-bit outputs equal to the rounded oracle."""
+    rng = np.random.default_rng(2000 + seed)
+    M = int(rng.integers(1, 9001))
+    N = int(rng.choice([int(rng.integers(1, 700)), 256 * int(rng.integers(1, 17))]))
+    K = 64 * int(rng.integers(1, 9))
+    bias = bool(seed % 2)
+    mode = ["f32", "bf16", "f16", "epi1"][seed % 4]
+    print(f"[gemm sweep] seed={seed} M={M} N={N} K={K} bias={bias} mode={mode}", flush=True)
+    m_pad = (M + 63) // 64 * 64
+    tn = next(t for t in (256, 128, 64, 32, 16, 8, 4, 2, 1) if N % t == 0)  # the launcher's tile check
+    a, sa, q, sw, b = make(rng, M, N, K, m_pad=m_pad, bias=bias)
+    v = og.epilogue(og.int_product(a[:M], q), sa[:M], sw, b)
+    if mode == "epi1":
+        x0 = rng.standard_normal((m_pad, N)).astype(np.float32)
+        types = rng.integers(0, 3, size=m_pad).astype(np.uint8)
+        gates = rng.standard_normal((3, N)).astype(np.float32)
+        wt = ops.QWeight("q8", gpu.upload(q), gpu.upload(sw), N, K, bias=gpu.upload(b) if bias else None)
+        X = gpu.upload(x0)
+        ops.gemm(gpu, gpu.upload(a), wt, X, M, sa=gpu.upload(sa), epi=1, rtype=gpu.upload(types),
+                 gate=gpu.upload(gates), tile=(64, tn, 8))
+        gpu.wait()
+        want = og.residual(x0[:M], v, gates, types[:M])
+        assert np.array_equal(X.numpy()[:M].view(np.uint32), want.view(np.uint32))
+        return
+    got = run(gpu, a, sa, q, sw, b, M, out_dtype=mode, tile=(64, tn, 4))
+    if mode == "f32":
+        assert np.array_equal(got.view(np.uint32), v.view(np.uint32))
+    elif mode == "bf16":
+        assert np.array_equal(got, to_bf16(v))
+    else:
+        assert np.array_equal(got.view(np.uint16), v.astype(np.float16).view(np.uint16))
+
+
 def test_refusals(gpu):
     rng = np.random.default_rng(44)
     a, sa, q, sw, _ = make(rng, 64, 256, 256)
