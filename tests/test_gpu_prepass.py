@@ -51,6 +51,43 @@ def outlier_rows(rng, S, H, hd, n_out=4, mult=20.0):
     return x.reshape(S, 3 * H * hd)
 
 
+ROT_CHOICES = {128: [0, 8, 24, 40, 64, 96, 128], 64: [0, 4, 12, 24, 32, 48, 64]}  # both lane layouts
+
+
+@pytest.mark.parametrize("seed", range(16))
+def test_random_shape_sweep_bit_exact(gpu, seed):
+    """A seeded sweep of pre-pass shapes: head dim 64 / 128, Q/K/V head counts chosen independently, ragged row
+    counts, batched sequences (seq_len) or one, RMS norm on or off, RoPE widths of both lane layouts, the
+    rotation on or off, bf16 / f16 / f32 input: int8 codes and scales bit for bit, V equal to its bf16 rounding."""
+    rng = np.random.default_rng(3000 + seed)
+    hd = [128, 64][seed % 2]
+    rot = int(rng.choice(ROT_CHOICES[hd]))
+    in_dt = ["bf16", "f16", "f32"][seed % 3]
+    norm, qk_rot = bool(rng.integers(0, 2)), bool(seed % 4 != 1)
+    Hq, Hk, Hv = (int(x) for x in rng.integers(1, 9, 3))
+    M = int(rng.integers(1, 700))
+    seq_len = int(rng.integers(1, M + 1)) if seed % 3 == 2 else None
+    out_rows = ((seq_len or M) + 63) // 64 * 64 + int(rng.integers(0, 2)) * 64
+    x = (rng.standard_normal((M, (Hq + Hk + Hv) * hd)) * 2).astype(np.float32)
+    x[:, rng.choice(x.shape[1], 5, replace=False)] *= 20  # a few outlier channels
+    xh = to_bf16(x) if in_dt == "bf16" else x.astype(np.float16) if in_dt == "f16" else x
+    wq, wk = rng.uniform(0.5, 1.5, (2, hd)).astype(np.float32)
+    ang = rng.uniform(0, 6.28, (M, max(rot // 2, 1)))
+    cs, sn = np.cos(ang).astype(np.float32), np.sin(ang).astype(np.float32)
+    kw = dict(wq=wq, wk=wk) if norm else {}
+    if rot:
+        kw.update(cs=cs, sn=sn)
+    got = run_prepass(gpu, xh, in_dt, M=M, Hq=Hq, Hk=Hk, Hv=Hv, hd=hd, out_rows=out_rows, rot=rot, norm=norm,
+                      eps=1e-6, qk_rot=qk_rot, seq_len=seq_len, **kw)
+    want = op.qk_norm_rope(as_float(xh, in_dt), Hq=Hq, Hk=Hk, Hv=Hv, hd=hd, out_rows=out_rows, rot=rot, eps=1e-6,
+                           norm=norm, seq_len=seq_len, q8=True, qk_rot=qk_rot, **kw)
+    for n in ("Q", "K"):
+        assert np.array_equal(got[n], want[n]), n
+    for n in ("qs", "ks"):
+        assert np.array_equal(got[n].view(np.uint32), want[n].view(np.uint32)), n
+    assert np.array_equal(got["V"].view(np.uint16), to_bf16(want["V"]))
+
+
 def test_golden_fixture_bit_exact(gpu):
     f = np.load(os.path.join(GOLDEN, "prepass_rot_int8.npz"))
     H, hd, out_rows = int(f["H"]), int(f["hd"]), int(f["out_rows"])
