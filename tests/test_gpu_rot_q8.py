@@ -47,6 +47,25 @@ def test_codes_and_scales_bit_exact(gpu, dt, M, D):
     assert np.array_equal(codes, wc)
 
 
+@pytest.mark.parametrize("seed", range(12))
+def test_random_shape_sweep_bit_exact(gpu, seed):
+    """A seeded sweep: widths of 1 to 56 Hadamard blocks of 256, up to 3000 rows, three input types, some rows
+    with outlier channels or all zeros: codes and scales bit for bit."""
+    rng = np.random.default_rng(4000 + seed)
+    dt = ["bf16", "f16", "f32"][seed % 3]
+    D = 256 * int(rng.integers(1, 57))
+    M = int(rng.integers(1, 3001))
+    x = (rng.standard_normal((M, D)) * 2).astype(np.float32)
+    x[rng.integers(0, M, 3)[:, None], rng.integers(0, D, 4)[None, :]] *= 50  # outliers
+    x[rng.integers(0, M)] = 0
+    xh = to_bf16(x) if dt == "bf16" else x.astype(np.float16) if dt == "f16" else x
+    xf = from_bf16(xh) if dt == "bf16" else xh.astype(np.float32)
+    codes, sa = run_rot(gpu, xh, dt, M, D)
+    wc, ws, _ = orq.rot_q8(xf, D)
+    assert np.array_equal(sa.view(np.uint32), ws.view(np.uint32))
+    assert np.array_equal(codes, wc)
+
+
 @pytest.mark.parametrize("dt", ["bf16", "f32"])
 def test_rotated_half_output_exact(gpu, dt):
     rng = np.random.default_rng(11)
