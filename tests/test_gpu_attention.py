@@ -631,3 +631,18 @@ def test_int8_three_group_kernel_edges(gpu, Lq, L, groups):
     err = np.abs(got[:Lq] - ref)
     assert err.max() < NS_MAX and err.mean() < NS_MEAN, (err.max(), err.mean())
     assert (got[Lq:] == 0).all()
+
+
+def test_key_count_beyond_32bit_offsets_refused(gpu):
+    """The wave kernel addresses K/V rows with 32-bit byte offsets: a key count whose V bytes (plus the blocks
+    the pipeline stages past the end) pass 4 GiB is refused before anything is launched."""
+    from h3metal_amd.gpu import GpuError
+    D, L = 128, (1 << 32) // 256 - 255  # (L + 256) * 256 bytes > 2^32
+    k_rows = (L + 31) // 32 * 32
+    Q, K, V = gpu.empty((1, 64, D), "i8"), gpu.empty((1, k_rows, D), "i8"), gpu.empty((1, k_rows, D), "bf16")
+    qs, ks = gpu.empty((1, 64), "f32"), gpu.empty((1, k_rows), "f32")
+    O = gpu.empty((64, D), "bf16")
+    print(f"[attention] refusal L={L}", flush=True)
+    with pytest.raises(GpuError, match="32-bit"):
+        ops.attention(gpu, Q, K, V, O, Lq=1, L=L, H=1, KVH=1, D=D, q_rows=64, k_rows=k_rows, scale=D ** -0.5,
+                      q_scale=qs, k_scale=ks)
