@@ -56,8 +56,8 @@ def scan(text: str, name: str = "<asm>") -> list[str]:
         if op.startswith("v_mfma"):
             dst = _regs(args[0])
             for r in set().union(*[_regs(a) for a in args[1:]]):
-                if r in recent and recent[r] < VALU_TO_MFMA and r not in dst:
-                    problems.append(f"{name}:{ln}: VALU write of {r} {recent[r]} wait states before: {s}")
+                if r in recent and recent[r] - 1 < VALU_TO_MFMA and r not in dst:
+                    problems.append(f"{name}:{ln}: VALU write of {r} {recent[r] - 1} wait states before: {s}")
             # an MFMA of the same opcode that accumulates onto exactly the registers an inline-assembly MFMA wrote
             # (srcC = that vdst) needs no wait states (the matrix unit forwards the result); every other access
             # of pending registers is a hazard
@@ -75,7 +75,7 @@ def scan(text: str, name: str = "<asm>") -> list[str]:
                     asm_dst.pop(r, None)
             if in_asm:
                 for r in dst:
-                    pending[r] = XDL_WAIT
+                    pending[r] = XDL_WAIT + 1  # reads k + 1 after k wait states: clear once k >= XDL_WAIT
                     asm_dst[r] = (op, args[0])
         elif not op.startswith("s_"):
             used = set().union(*[_regs(a) for a in args]) if args else set()
@@ -92,7 +92,7 @@ def scan(text: str, name: str = "<asm>") -> list[str]:
                 del pending[r]
         for r in list(recent):
             recent[r] += ws
-            if recent[r] > 2 * VALU_TO_MFMA:
+            if recent[r] > VALU_TO_MFMA + 1:
                 del recent[r]
     return problems
 

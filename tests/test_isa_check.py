@@ -1,0 +1,56 @@
+"""The build-time hazard check of inline-assembly MFMAs (h3metal_amd/isa_check.py) on small hand-written
+assembly listings: each hazard it exists for is reported, and the patterns it must accept (enough wait states,
+back-to-back accumulation onto the same registers) are not."""
+
+from h3metal_amd.isa_check import XDL_WAIT, scan
+
+ASM_MFMA = """;;#ASMSTART
+v_mfma_f32_32x32x16_bf16 a[0:15], v[0:3], v[4:7], a[0:15]
+;;#ASMEND"""
+
+
+def listing(*lines):
+    return "\n".join(["kern:"] + list(lines))
+
+
+def test_valu_read_of_a_pending_accumulator_is_reported():
+    bad = scan(listing(ASM_MFMA, "v_accvgpr_read_b32 v8, a3"))
+    assert len(bad) == 1 and "a', 3" in bad[0]
+
+
+def test_enough_wait_states_clear_the_accumulator():
+    assert XDL_WAIT == 18  # a 16-pass XDL result, read or overwritten by another instruction
+    # s_nop N is N + 1 wait states
+    assert scan(listing(ASM_MFMA, "s_nop 7", "s_nop 7", "s_nop 1", "v_accvgpr_read_b32 v8, a3")) == []
+    assert scan(listing(ASM_MFMA, *(["v_add_f32 v9, v9, v9"] * XDL_WAIT), "v_accvgpr_read_b32 v8, a3")) == []
+    # one wait state short
+    assert len(scan(listing(ASM_MFMA, "s_nop 7", "s_nop 7", "s_nop 0", "v_accvgpr_read_b32 v8, a3"))) == 1
+    assert len(scan(listing(ASM_MFMA, *(["v_add_f32 v9, v9, v9"] * (XDL_WAIT - 1)),
+                            "v_accvgpr_read_b32 v8, a3"))) == 1
+
+
+def test_back_to_back_accumulation_is_accepted():
+    same = "v_mfma_f32_32x32x16_bf16 a[0:15], v[8:11], v[12:15], a[0:15]"
+    assert scan(listing(ASM_MFMA, same)) == []
+    assert scan(listing(ASM_MFMA, ";;#ASMSTART", same, ";;#ASMEND", same)) == []
+
+
+def test_other_reads_of_a_pending_accumulator_are_reported():
+    # another opcode accumulating onto it, a partial overlap of srcC, the accumulator as a multiplicand
+    other = "v_mfma_f32_32x32x8_f16 a[0:15], v[8:9], v[10:11], a[0:15]"
+    part = "v_mfma_f32_32x32x16_bf16 a[16:31], v[8:11], v[12:15], a[8:23]"
+    mult = "v_mfma_f32_32x32x16_bf16 a[16:31], a[0:3], v[12:15], a[16:31]"
+    for line in (other, part, mult):
+        assert len(scan(listing(ASM_MFMA, line))) == 1, line
+
+
+def test_valu_write_just_before_an_mfma_operand_is_reported():
+    w = "v_mov_b32 v5, 0"
+    mfma = "v_mfma_f32_32x32x16_bf16 a[32:47], v[0:3], v[4:7], a[32:47]"
+    assert len(scan(listing(w, mfma))) == 1
+    assert len(scan(listing(w, "s_nop 0", mfma))) == 1
+    assert scan(listing(w, "s_nop 1", mfma)) == []
+
+
+def test_a_new_function_starts_clean():
+    assert scan(listing(ASM_MFMA) + "\nother_kern:\nv_accvgpr_read_b32 v8, a3") == []
