@@ -47,6 +47,23 @@ def test_codes_and_scales_bit_exact(gpu, dt, M, D):
     assert np.array_equal(codes, wc)
 
 
+@pytest.mark.parametrize("mag", [2e-37, 1e-36, 1e-33, 1e-20, 1.0, 1e4])
+@pytest.mark.parametrize("dt", ["f32", "bf16"])
+def test_tiny_and_large_rows_bit_exact(gpu, mag, dt):
+    """Rows from 2e-37 (rotated values partly subnormal, 1 / scale near the float range's top) to 1e4: codes and
+    scales bit for bit."""
+    rng = np.random.default_rng(int(-np.log10(mag) * 10) + 500)
+    M, D = 8, 1024
+    x = (rng.standard_normal((M, D)) * mag).astype(np.float32)
+    xh = to_bf16(x) if dt == "bf16" else x
+    xf = from_bf16(xh) if dt == "bf16" else xh
+    codes, sa = run_rot(gpu, xh, dt, M, D)
+    wc, ws, _ = orq.rot_q8(xf, D)
+    assert np.isfinite(ws).all() and np.isfinite(1 / ws).all()
+    assert np.array_equal(sa.view(np.uint32), ws.view(np.uint32))
+    assert np.array_equal(codes, wc)
+
+
 @pytest.mark.parametrize("seed", range(12))
 def test_random_shape_sweep_bit_exact(gpu, seed):
     """A seeded sweep: widths of 1 to 56 Hadamard blocks of 256, up to 3000 rows, three input types, some rows
