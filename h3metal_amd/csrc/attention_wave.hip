@@ -18,11 +18,12 @@ namespace {
 //     P V of block j-1 (8 MFMAs) | softmax of block j (16 scores per lane) | S of block j+1 (4 to 8 MFMAs)
 // Each sub-tile's score registers are overwritten by block j+1 right after block j's softmax read them, and
 // its P registers by block j right after block j-1's P V read them, so no register set is double-buffered.
-// The running maximum is checked after the exponentials: a block whose per-lane row sum exceeds 2^16 (some
-// score more than ~11 log2 units above the reference maximum; also inf or NaN) or that meets the first valid
-// keys is recomputed in a rare branch from its K and scales (still in their LDS ring slots) with the exact
-// block maximum, after O and l are rescaled. P is bf16 (fp32's exponent range), so a reference up to 2^16 below
-// the true maximum loses no precision.
+// The running maximum is checked after the exponentials: a block whose per-lane row sum exceeds the limit
+// (2^30 with bf16 P: scores up to ~30 log2 units above the reference maximum pass; 2^15 with f16 P, whose
+// largest finite value is 65504; also inf or NaN) or that meets the first valid keys is recomputed in a rare
+// branch from its K and scales (still in their LDS ring slots) with the exact block maximum, after O and l are
+// rescaled. A reference maximum below the true one only scales P by a power of two: P keeps its relative
+// rounding, and the fp32 O and l keep their range (a row's l stays below 2^30 per key block).
 // Staging: LDS-direct buffer loads two blocks ahead into 4-deep rings; one barrier per key block.
 // P V MFMA with the O accumulator in AGPRs. Written as assembly so that only O (and Q, an operand the score
 // MFMAs read from AGPRs) lives in the accumulation registers: the score MFMAs are built with VGPR results
@@ -63,7 +64,9 @@ constexpr int NU = WAVE_NU;         // 32-query MFMA tiles per wave (sharing eve
 constexpr int BQV = WAVE_BQ;        // query rows per workgroup
 static_assert(BQV == NWV * 32 * NU, "32 NU query rows per wave");
 constexpr int NRV = 4;              // ring depth (blocks)
-constexpr float SUM_LIMIT = 65536.0f;
+// accepted growth of a row sum per key block: bf16 P (fp32's exponent range) and f16 P (largest finite 65504)
+template <int VT>
+constexpr float sum_limit() { return VT == T_F16 ? 0x1p15f : 0x1p30f; }
 // int8 score accumulators start from the bits of the float 1/(2 pi) (an inline constant of the MFMA's C operand,
 // so the seed costs no register): with |q . k| <= 128 * 127^2 < 2^21 the sum stays inside that float's binade
 // [2^-3, 2^-2), whose ulp is 2^-26, so the accumulator's bits ARE the float SEED_F + s * 2^-26 and
@@ -538,10 +541,10 @@ void attention_wave_kernel(const char *__restrict__ Q, const char *__restrict__ 
       tick(idx < 3 ? idx : 2);
       if (t == 1) {
         // block j's row sums are the growth of the running partial sums; query tile u's are complete here. A
-        // sum above SUM_LIMIT (or NaN) means a score far above the reference maximum: the block is recomputed
+        // sum above the limit (or NaN) means a score far above the reference maximum: the block is recomputed
         // below
         tot[u] = (la[u][0] + la[u][1]) + (la[u][2] + la[u][3]);
-        bad = bad | !(tot[u] - l[u] <= SUM_LIMIT);
+        bad = bad | !(tot[u] - l[u] <= sum_limit<VT>());
       }
     }
     // this wave's loads of the previous step (this step's V loads, the newest, may still be in flight)
@@ -558,7 +561,7 @@ void attention_wave_kernel(const char *__restrict__ Q, const char *__restrict__ 
     if constexpr (QK8 && SEEDED) ((float *)(smem + C::COFF))[((j + 2) % NRV) * BK + lane] = kv * -SEED_F;
     tick(4);
     tot[NU - 1] = (la[NU - 1][0] + la[NU - 1][1]) + (la[NU - 1][2] + la[NU - 1][3]);
-    bad = bad | !(tot[NU - 1] - l[NU - 1] <= SUM_LIMIT);
+    bad = bad | !(tot[NU - 1] - l[NU - 1] <= sum_limit<VT>());
 #ifdef WAVE_NO_CHECK
     bad = false;
 #endif

@@ -646,3 +646,40 @@ def test_key_count_beyond_32bit_offsets_refused(gpu):
     with pytest.raises(GpuError, match="32-bit"):
         ops.attention(gpu, Q, K, V, O, Lq=1, L=L, H=1, KVH=1, D=D, q_rows=64, k_rows=k_rows, scale=D ** -0.5,
                       q_scale=qs, k_scale=ks)
+
+
+@pytest.mark.parametrize("path", ["int8", "bf16", "f16"])
+def test_scores_rising_far_above_the_first_block(gpu, path):
+    """Key scores that rise by ~100 log2 units from the first keys to the last (a ramp on one channel shared by
+    every query), so that each row's reference maximum is passed by more than the accepted growth several times
+    (2^30 per block with bf16 P, 2^15 with f16 P): the recomputed blocks and the rescaled O and l against float64
+    attention, at the north-star tolerance."""
+    rng = np.random.default_rng(77)
+    H, Lq, L, D = 2, 130, 1100, 128
+    q = rng.standard_normal((H, Lq, D)).astype(np.float32)
+    k = rng.standard_normal((H, L, D)).astype(np.float32)
+    v = rng.standard_normal((H, L, D)).astype(np.float32)
+    q[..., 0] = 8.0
+    k[..., 0] = np.linspace(-50.0, 50.0, L, dtype=np.float32)
+    if path == "int8":
+        qi, qs = q8(q)
+        ki, ks = q8(k)
+        vb = to_bf16(v)
+        got = run_attention(gpu, qi, ki, vb, dtype="bf16", Lq=Lq, L=L, H=H, KVH=H, D=D, scale=D ** -0.5, qs=qs,
+                            ks=ks, out_dt="f32")
+        ref = oa.ref_attention(qi * qs[..., None].astype(np.float64), ki * ks[..., None].astype(np.float64),
+                               from_bf16(vb), D ** -0.5)
+    elif path == "bf16":
+        qb, kb, vb = to_bf16(q), to_bf16(k), to_bf16(v)
+        got = run_attention(gpu, qb, kb, vb, dtype="bf16", Lq=Lq, L=L, H=H, KVH=H, D=D, scale=D ** -0.5,
+                            out_dt="f32")
+        ref = oa.ref_attention(from_bf16(qb), from_bf16(kb), from_bf16(vb), D ** -0.5)
+    else:
+        qh, kh, vh = q.astype(np.float16), k.astype(np.float16), v.astype(np.float16)
+        got = run_attention(gpu, qh, kh, vh, dtype="f16", Lq=Lq, L=L, H=H, KVH=H, D=D, scale=D ** -0.5,
+                            out_dt="f32")
+        ref = oa.ref_attention(qh, kh, vh, D ** -0.5)
+    got = got[:Lq]
+    err = np.abs(got - ref)
+    assert np.isfinite(got).all()
+    assert err.max() < NS_MAX and err.mean() < NS_MEAN, (err.max(), err.mean())
