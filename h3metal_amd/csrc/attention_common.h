@@ -142,33 +142,46 @@ __global__ __launch_bounds__(256) void attention_merge(const float *__restrict__
   const float *w0 = ws + ((size_t)tr * s * BQ + r) * (DG + 4);
   const size_t ustride = (size_t)BQ * (DG + 4);
   float mx = -INFINITY;
+#pragma unroll 4
   for (int c = 0; c < s; c++) mx = fmaxf(mx, w0[c * ustride + DG]);
-  float lsum = 0.0f, acc[PER];
-#pragma unroll
-  for (int i = 0; i < PER; i++) acc[i] = 0.0f;
+  // lane l holds PER contiguous channels from PER l (one 4- or 8-byte load per chunk; the loops unrolled so that
+  // the loads of several chunks are in flight at once)
+  static_assert(PER <= 2 && DG % PER == 0, "one or two channels per lane");
+  const int d0 = PER * lane;
+  const bool dok = d0 < DG;
+  float lsum = 0.0f, acc[2] = {0.0f, 0.0f};
+#pragma unroll 4
   for (int c = 0; c < s; c++) {
     const float *wr = w0 + c * ustride;
     const float mc = wr[DG];
     const float wt = mc == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(mc - mx);
     lsum += wt * wr[DG + 1];
-#pragma unroll
-    for (int i = 0; i < PER; i++) {
-      const int d = lane + 64 * i;
-      if (d < DG) acc[i] += wt * wr[d];
+    if (dok) {
+      if constexpr (PER == 2) {
+        const float2 v = *(const float2 *)(wr + d0);
+        acc[0] += wt * v.x;
+        acc[1] += wt * v.y;
+      } else {
+        acc[0] += wt * wr[d0];
+      }
     }
   }
   const float inv = lsum > 0.0f ? 1.0f / lsum : 0.0f;
   constexpr int OSZ = OT == T_F32 ? 4 : 2;
   const int seq = h / p.seq_heads;
   char *orow = O + (((size_t)seq * p.seq_rows + q) * p.o_stride + (size_t)(h - seq * p.seq_heads) * DG) * OSZ;
-#pragma unroll
-  for (int i = 0; i < PER; i++) {
-    const int d = lane + 64 * i;
-    if (d < DG) {
-      const float v = acc[i] * inv;
-      if constexpr (OT == T_F32) *(float *)(orow + d * 4) = v;
-      else if constexpr (OT == T_BF16) *(__bf16 *)(orow + d * 2) = (__bf16)v;
-      else *(_Float16 *)(orow + d * 2) = (_Float16)v;
+  if (dok) {
+    const float v0 = acc[0] * inv, v1 = acc[1] * inv;
+    if constexpr (PER == 1) {
+      if constexpr (OT == T_F32) *(float *)(orow + d0 * 4) = v0;
+      else if constexpr (OT == T_BF16) *(__bf16 *)(orow + d0 * 2) = (__bf16)v0;
+      else *(_Float16 *)(orow + d0 * 2) = (_Float16)v0;
+    } else if constexpr (OT == T_F32) {
+      *(float2 *)(orow + d0 * 4) = make_float2(v0, v1);
+    } else if constexpr (OT == T_BF16) {
+      *(bf16x2 *)(orow + d0 * 2) = bf16x2{(__bf16)v0, (__bf16)v1};
+    } else {
+      *(f16x2 *)(orow + d0 * 2) = f16x2{(_Float16)v0, (_Float16)v1};
     }
   }
 }
