@@ -46,10 +46,11 @@
 //    LDS at the end of its second half-step.
 //  * The 1-D grid is remapped so that each XCD (own L2) runs a contiguous
 //    range of (head, query-block) tiles, which then share one head's K/V in L2.
-//  * int8 scores at D = 128 without a causal mask (the DiT path) run on a
-//    three-group variant (attention3_kernel below: 12 waves, one in its matrix
-//    phase and two in softmax slots per SIMD at any time, LDS-direct staging);
-//    the macro GROUPS=2 keeps them on the two-group kernel.
+//  * D = 128 without a causal mask (the DiT path) runs on the wave-pipelined
+//    kernel of attention_wave.hip by default; the macro GROUPS=3 selects the
+//    three-group variant below for int8 scores (attention3_kernel: 12 waves, one
+//    in its matrix phase and two in softmax slots per SIMD at any time,
+//    LDS-direct staging) and GROUPS=2 this file's two-group kernel.
 #include "attention_common.h"
 
 #include <algorithm>
