@@ -46,11 +46,12 @@
 //    LDS at the end of its second half-step.
 //  * The 1-D grid is remapped so that each XCD (own L2) runs a contiguous
 //    range of (head, query-block) tiles, which then share one head's K/V in L2.
-//  * D = 128 without a causal mask (the DiT path) runs on the wave-pipelined
-//    kernel of attention_wave.hip by default; the macro GROUPS=3 selects the
-//    three-group variant below for int8 scores (attention3_kernel: 12 waves, one
-//    in its matrix phase and two in softmax slots per SIMD at any time,
-//    LDS-direct staging) and GROUPS=2 this file's two-group kernel.
+//  * D = 128 without a causal mask (the DiT path) runs on other kernels by
+//    default: int8 scores on the paired kernel of attention_pair.hip (two waves
+//    per SIMD), 16-bit scores on the wave-pipelined kernel of
+//    attention_wave.hip. The macro GROUPS selects a kernel for A/B tests:
+//    1 the wave-pipelined one, 2 this file's two-group kernel, 3 the paired one
+//    (int8 scores only).
 #include "attention_common.h"
 
 #include <algorithm>
@@ -496,352 +497,14 @@ __global__ __launch_bounds__(NW * 64) void attention_kernel(const char *__restri
   }
 }
 
-// ---------------------------------------------------------------------------------------------------------------
-// Three-group variant for int8 scores, D = 128, no causal mask: 12 waves, three groups of 4 (waves w, w + 4,
-// w + 8: the waves of a workgroup are placed on the 4 SIMDs in turn, so each SIMD holds one wave of each group),
-// 384 query rows per workgroup. Each key block is three slots separated by barriers; group g runs its matrix
-// phase (P V of block j-1, then the scores of block j) in slot 3j + g and its vector phase in the two slots after
-// it (conversion, maximum and lazy rescale; then P and the row sums). At any time one wave of a SIMD issues MFMAs
-// and two issue softmax VALU work, so the VALU pipe is fed from two instruction streams instead of one (measured
-// about 1% faster than the two-group kernel at config 4; the matrix slot is the longer one).
-// Staging is LDS-direct (buffer_load ... lds, no registers): in slot 3j + g, group 0 loads K and the key scales of
-// block j + 2, groups 1 and 2 the two halves of V of block j + 1, into 3-deep rings (scales 4-deep); a wave waits
-// for its loads at the start of its next matrix phase, and the barrier ending that slot publishes them before
-// the first reader (group 0's matrix phase of block j + 2, slot 3j + 6).
-constexpr int NW3 = 12;
-
-struct Cfg3 {
-  static constexpr int D = 128, RB = 128, NP = 8, NCH = 4;
-  static constexpr int NT = NW3 * 64, BQ = NW3 * 32;
-  static constexpr int KBYTES = BK * RB, VBYTES = BK * D * 2;
-  static constexpr int KOFF = 0, VOFF = 3 * KBYTES, SOFF = VOFF + 3 * VBYTES;
-  static constexpr int QOFF = SOFF + 4 * BK * 4;  // each wave's Q operand: 4 chunks x 64 lanes x 16 bytes
-  static constexpr int LDS = QOFF + NW3 * 4096;
-};
-
-// DUMP: instead of attention, write this kernel's raw int32 score accumulators S[h][q][key], for tests.
-template <int VT, int OT, bool DUMP>
-__global__ __launch_bounds__(NW3 * 64) void attention3_kernel(const char *__restrict__ Q, const char *__restrict__ K,
-                                                              const char *__restrict__ V, char *__restrict__ O,
-                                                              const float *__restrict__ qs,
-                                                              const float *__restrict__ ks, AttnParams p, int nqb,
-                                                              Split sp) {
-  using C = Cfg3;
-  constexpr int D = C::D;
-  using VT8 = typename Vec8<VT>::type;
-  using VE = typename Vec8<VT>::elem;
-  using VP2 = typename Vec8<VT>::pair;
-  extern __shared__ __attribute__((aligned(16))) char smem[];
-  const unsigned lds0 = (unsigned)(size_t)(__attribute__((address_space(3))) char *)smem;
-
-  const int tid = threadIdx.x, lane = tid & 63, hl = lane >> 5, l32 = lane & 31;
-  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int grp = w >> 2, wl = w & 3;  // group (0, 1, 2: its slot within each key block), wave within the group
-  const int b = blockIdx.x;
-  int lid, unit = -1;
-  if (b < sp.nfull) {
-    const int nb = sp.nfull;
-    const int per = nb >> 3, rem = nb & 7, xcd = b & 7, loc = b >> 3;
-    lid = (xcd < rem ? xcd * (per + 1) : rem * (per + 1) + (xcd - rem) * per) + loc;
-  } else {
-    unit = b - sp.nfull;
-    lid = sp.nfull + unit / sp.s;
-  }
-  const int h = lid / nqb, qb = lid - h * nqb;
-  const int kvh = h / (p.H / p.KVH);
-  const int q = qb * C::BQ + w * 32 + l32;
-  const bool qvalid = q < p.Lq;
-
-  // the Q operand lives in LDS (this wave's own 4 KB), read back for each block's score MFMAs: its 16
-  // registers go to a deeper V operand prefetch
-  char *qlds = smem + C::QOFF + w * 4096 + lane * 16;
-  {
-    const char *qrow = Q + ((size_t)h * p.q_rows + (qvalid ? q : 0)) * C::RB;
-#pragma unroll
-    for (int c = 0; c < C::NCH; c++) {
-      const i32x4 v = *(const i32x4 *)(qrow + (2 * c + hl) * 16);
-      *(i32x4 *)(qlds + c * 1024) = qvalid ? v : i32x4{0, 0, 0, 0};
-    }
-  }
-  const float qsc = qvalid ? fmaxf(qs[(size_t)h * p.q_rows + q] * p.scale, FLT_MIN) : 1.0f;
-
-  int key0 = 0, Lk = p.L;
-  if (unit >= 0) {
-    key0 = (unit % sp.s) * sp.cb * BK;
-    Lk = min(p.L, key0 + sp.cb * BK) - key0;
-  }
-  const char *Kh = K + ((size_t)kvh * p.k_rows + key0) * C::RB;
-  const char *Vh = V + ((size_t)kvh * p.k_rows + key0) * D * 2;
-  const float *ksh = ks + (size_t)kvh * p.k_rows + key0;
-  const int nblk = Lk > 0 ? (Lk + BK - 1) / BK : 0;
-
-  // -- LDS-direct staging. A wave's load instruction writes 64 x 16 bytes at M0 + 16 lane; each lane fetches the
-  // piece whose swizzled LDS position that is. Rows at or past Lk read as zero (descriptor range).
-  auto rsrc = [&](const void *base, int blk, int row_bytes) {
-    const int rows = max(0, Lk - blk * BK);
-    return __builtin_amdgcn_make_buffer_rsrc((void *)((const char *)base + (size_t)blk * BK * row_bytes), (short)0,
-                                             __builtin_amdgcn_readfirstlane(rows * row_bytes), 0x00020000);
-  };
-  unsigned goff[2];  // global byte offsets of this lane's two pieces within a block (K for group 0, V otherwise)
-#pragma unroll
-  for (int r = 0; r < 2; r++) {
-    const int c = r * 4 + wl;
-    if (grp == 0) {
-      const int o = c * 1024 + 16 * lane;
-      const int row = o >> 7, slot = (o >> 4) & 7;
-      goff[r] = row * C::RB + (slot ^ kswz<C::RB, C::NP>(row)) * 16;
-    } else {
-      const int o = (grp - 1) * 8192 + c * 1024 + 16 * lane;
-      const int row = o >> 8, uu = (o & 255) >> 5, sub = (o >> 4) & 1;
-      goff[r] = row * (D * 2) + (2 * (uu ^ (2 * (row & 3))) + sub) * 16;
-    }
-  }
-  auto stage_k = [&](int blk) {  // group 0: K and key scales of block blk
-    const __amdgpu_buffer_rsrc_t r = rsrc(Kh, blk, C::RB);
-#pragma unroll
-    for (int rr = 0; rr < 2; rr++)
-      dma16(lds0 + C::KOFF + (blk % 3) * C::KBYTES + (rr * 4 + wl) * 1024, goff[rr], r);
-    if (wl == 0) dma4(lds0 + C::SOFF + (blk & 3) * BK * 4, lane * 4, rsrc(ksh, blk, 4));
-  };
-  auto stage_v = [&](int blk) {  // groups 1, 2: their half of V of block blk
-    const __amdgpu_buffer_rsrc_t r = rsrc(Vh, blk, D * 2);
-#pragma unroll
-    for (int rr = 0; rr < 2; rr++)
-      dma16(lds0 + C::VOFF + (blk % 3) * C::VBYTES + (grp - 1) * 8192 + (rr * 4 + wl) * 1024, goff[rr], r);
-  };
-
-  f32x16 o[D / 32];
-#pragma unroll
-  for (int db = 0; db < D / 32; db++)
-#pragma unroll
-    for (int i = 0; i < 16; i++) o[db][i] = 0.0f;
-  float m = -INFINITY, l = 0.0f;
-  i32x16 s[2];
-  VT8 pb[2][2];
-#pragma unroll
-  for (int t = 0; t < 2; t++)
-#pragma unroll
-    for (int i = 0; i < 16; i++) {
-      s[t][i] = 0;
-      pb[t][i >> 3][i & 7] = (VE)0.0f;
-    }
-  const int krow = 16 * (l32 >> 4) + 8 * ((l32 >> 2) & 1) + 4 * ((l32 >> 3) & 1) + (l32 & 3);
-  const int l16 = lane & 15;
-  const int tr_row = l16 >> 2, tr_col = (l16 & 3) * 8;
-
-  // LDS read addresses. V (transposing reads): lane part key * 256 + tr_col for the step's first key, and the
-  // swizzled 32-byte unit 2 (db ^ (key % 4)) + half of channel block db, so one base per db and constant offsets
-  // for the step and the second 4 keys. K: one base per chunk c (the swizzle depends on the lane's row only).
-  // The bases are made opaque in each matrix phase, so the compiler keeps 8 registers instead of hoisting one
-  // per read out of the loop.
-  unsigned vbase[D / 32], kbase[C::NCH];
-  {
-    const int k0 = 8 * hl + tr_row;
-#pragma unroll
-    for (int db = 0; db < D / 32; db++) vbase[db] = voff<D>(k0, (db * 32 + (l32 & 16)) / 8) + tr_col;
-#pragma unroll
-    for (int c = 0; c < C::NCH; c++) kbase[c] = krow * C::RB + (((2 * c + hl) ^ kswz<C::RB, C::NP>(krow)) * 16);
-  }
-
-  // matrix phase of block j: O^T += V(j-1)^T P(j-1)^T, then S(j) = K(j) Q^T (P V first: the scores' registers
-  // are free until then)
-  auto matrix_phase = [&](int j) {
-#pragma unroll
-    for (int db = 0; db < D / 32; db++) asm volatile("" : "+v"(vbase[db]));
-#pragma unroll
-    for (int c = 0; c < C::NCH; c++) asm volatile("" : "+v"(kbase[c]));
-    const unsigned *vb = vbase, *kb4 = kbase;
-    if (j >= 1) {
-      const char *Vs = smem + C::VOFF + ((j - 1) % 3) * C::VBYTES;
-      auto vload = [&](int st, i16x8 (&va)[D / 32]) {
-        const int t = st >> 1, s2 = st & 1;
-        const int koff = (32 * t + 16 * s2) * (D * 2);  // keys 32 t + 16 s2 + 8 hl + tr_row (+ 4)
-#pragma unroll
-        for (int db = 0; db < D / 32; db++) {
-          const i16x4 lo = lds_tr16(Vs + vb[db] + koff);
-          const i16x4 hi = lds_tr16(Vs + vb[db] + koff + 4 * (D * 2));
-          va[db] = i16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-        }
-      };
-      i16x8 va[2][D / 32];
-      vload(0, va[0]);
-#pragma unroll
-      for (int st = 0; st < 4; st++) {
-        if (st < 3) vload(st + 1, va[(st + 1) & 1]);
-        __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-        for (int db = 0; db < D / 32; db++) o[db] = mma_pv<VT>(va[st & 1][db], pb[st >> 1][st & 1], o[db]);
-      }
-    }
-    if (j < nblk) {
-      const char *Ks = smem + C::KOFF + (j % 3) * C::KBYTES;
-      i32x4 ka[2][C::NCH], qreg[C::NCH];
-#pragma unroll
-      for (int c = 0; c < C::NCH; c++) qreg[c] = *(const i32x4 *)(qlds + c * 1024);
-#pragma unroll
-      for (int t = 0; t < 2; t++)
-#pragma unroll
-        for (int c = 0; c < C::NCH; c++) ka[t][c] = *(const i32x4 *)(Ks + kb4[c] + 32 * t * C::RB);
-      // all 12 reads before the first score MFMA (the P V operands' registers are free by now; the scheduler
-      // would otherwise sink each read to its MFMA and expose its latency 8 times)
-      __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-      for (int t = 0; t < 2; t++)
-#pragma unroll
-        for (int c = 0; c < C::NCH; c++) s[t] = mma_qk<T_I8>(ka[t][c], qreg[c], c == 0 ? i32x16{} : s[t]);
-    }
-  };
-
-  // first vector slot of block j: the scores in log2 units before the query scale, written over their
-  // accumulators (float bits), masking, the block maximum and the lazy rescale
-  auto vector_a = [&](int j) {
-    if (j >= nblk) return;
-    const int kb = j * BK;
-    if constexpr (DUMP) {
-      // element i of lane-half hl holds key 64 j + 32 t + 16 (i / 8) + 8 hl + i % 8
-      if (qvalid) {
-#pragma unroll
-        for (int t = 0; t < 2; t++)
-#pragma unroll
-          for (int i = 0; i < 16; i++) {
-            const int key = kb + 32 * t + 16 * (i >> 3) + 8 * hl + (i & 7);
-            if (key < p.L) *((int *)O + ((size_t)h * p.Lq + q) * p.L + key) = s[t][i];
-          }
-      }
-      return;
-    }
-    const float *ksc = (const float *)(smem + C::SOFF) + (j & 3) * BK;
-    float am[2];
-#pragma unroll
-    for (int t = 0; t < 2; t++) {
-      f32x4 k4[2][2];
-#pragma unroll
-      for (int s8 = 0; s8 < 2; s8++)
-#pragma unroll
-        for (int hh = 0; hh < 2; hh++) k4[s8][hh] = *(const f32x4 *)(ksc + 32 * t + 16 * s8 + 8 * hl + 4 * hh);
-      // exact int32 scores from a zero-seeded accumulator; v_cvt_f32_i32 issues at the full VALU rate on gfx950,
-      // and a zero seed needs no registers (a 1.5 * 2^23 seed would hold 16 for the whole loop)
-      const i32x16 si = s[t];
-      f32x16 x;
-#pragma unroll
-      for (int s8 = 0; s8 < 2; s8++)
-#pragma unroll
-        for (int hh = 0; hh < 2; hh++)
-#pragma unroll
-          for (int e = 0; e < 4; e++) {
-            const int i = 8 * s8 + 4 * hh + e;
-            x[i] = (float)si[i] * k4[s8][hh][e];
-          }
-      if (kb + BK > Lk) {
-#pragma unroll
-        for (int i = 0; i < 16; i++)
-          if (kb + 32 * t + 16 * (i >> 3) + 8 * hl + (i & 7) >= Lk) x[i] = -INFINITY;
-      }
-      am[t] = -INFINITY;
-#pragma unroll
-      for (int i = 0; i < 16; i++) am[t] = fmaxf(am[t], x[i]);
-      s[t] = __builtin_bit_cast(i32x16, x);
-    }
-    const float amax = fmaxf(am[0], am[1]);
-    if (__any(amax * qsc > m + SLACK)) {
-      const float ap = fmaxf(amax, __shfl_xor(amax, 32));
-      const float mn = fmaxf(m, ap * qsc);
-      const float f = mn == -INFINITY ? 1.0f : __builtin_amdgcn_exp2f(m - mn);
-      m = mn;
-      l *= f;
-#pragma unroll
-      for (int db = 0; db < D / 32; db++)
-#pragma unroll
-        for (int i = 0; i < 16; i++) o[db][i] *= f;
-    }
-  };
-  // second vector slot: P(j) = 2^(x qsc - m), rounded to the value type, and the row sums of the rounded P
-  auto vector_b = [&](int j) {
-    if (DUMP || j >= nblk) return;
-    const float nm = m == -INFINITY ? 0.0f : -m;
-    float ls[2] = {0.0f, 0.0f};
-#pragma unroll
-    for (int t = 0; t < 2; t++) {
-      const f32x16 x = __builtin_bit_cast(f32x16, s[t]);
-#pragma unroll
-      for (int i = 0; i < 16; i += 2) {
-        const float p0 = __builtin_amdgcn_exp2f(fmaf(x[i], qsc, nm));
-        const float p1 = __builtin_amdgcn_exp2f(fmaf(x[i + 1], qsc, nm));
-        const VP2 pr = {(VE)p0, (VE)p1};
-        pb[t][i >> 3][i & 7] = pr[0];
-        pb[t][i >> 3][(i & 7) + 1] = pr[1];
-        ls[t] = sum2<VT>(pr, ls[t]);
-      }
-    }
-    l += ls[0] + ls[1];
-  };
-
-  // prologue: K and scales of blocks 0 and 1, V of block 0
-  if (grp == 0) {
-    stage_k(0);
-    stage_k(1);
-  } else {
-    stage_v(0);
-  }
-  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-  __syncthreads();
-  for (int i = 0; i < grp; i++) __syncthreads();
-  for (int j = 0; j <= nblk; j++) {
-    __builtin_amdgcn_s_setprio(3);
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this wave's loads from its previous matrix slot
-    matrix_phase(j);
-    if (grp == 0) stage_k(j + 2);  // ring slots of blocks j - 1 (K) and j - 2 (V): read before this slot
-    else stage_v(j + 1);
-    __builtin_amdgcn_s_setprio(0);
-    __syncthreads();
-    vector_a(j);
-    __syncthreads();
-    vector_b(j);
-    __syncthreads();
-  }
-  for (int i = grp; i < 2; i++) __syncthreads();
-  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // loads past the last block (zeros) land before the exit
-  if constexpr (DUMP) return;
-
-  const float lt = l + __shfl_xor(l, 32);
-  if (unit >= 0) {
-    float *wrow = sp.ws + ((size_t)unit * C::BQ + (q - qb * C::BQ)) * (D + 4);
-#pragma unroll
-    for (int db = 0; db < D / 32; db++)
-#pragma unroll
-      for (int g = 0; g < 4; g++)
-        store4<T_F32>((char *)(wrow + db * 32 + 8 * g + 4 * hl), o[db][4 * g], o[db][4 * g + 1], o[db][4 * g + 2],
-                      o[db][4 * g + 3]);
-    if (hl == 0) {
-      wrow[D] = m;
-      wrow[D + 1] = lt;
-    }
-    return;
-  }
-  const float inv = lt > 0.0f ? 1.0f / lt : 0.0f;
-  if (qvalid) {
-    constexpr int OSZ = OT == T_F32 ? 4 : 2;
-    const int seq = h / p.seq_heads;
-    char *orow = O + (((size_t)seq * p.seq_rows + q) * p.o_stride + (size_t)(h - seq * p.seq_heads) * D) * OSZ;
-#pragma unroll
-    for (int db = 0; db < D / 32; db++)
-#pragma unroll
-      for (int g = 0; g < 4; g++) {
-        const int d = db * 32 + 8 * g + 4 * hl;
-        store4<OT>(orow + d * OSZ, o[db][4 * g] * inv, o[db][4 * g + 1] * inv, o[db][4 * g + 2] * inv,
-                   o[db][4 * g + 3] * inv);
-      }
-  }
-}
-
-
 int esize(int t) { return t == T_I8 ? 1 : t == T_F32 ? 4 : 2; }
 
 }  // namespace
 
 // R partly filled tiles of a last round, cut into s <= CUs / R chunks: R * s <= CUs units of BQ rows of
-// (D + 4) floats, at the largest BQ (the three-group kernel's 384 rows) and D = 128.
-size_t attention_workspace_max(int cus) { return (size_t)std::max(cus, 1) * Cfg3::BQ * (128 + 4) * sizeof(float); }
+// (D + 4) floats at D = 128. The allowance per unit is 384 rows (more than any kernel's 256), which also leaves the
+// context's scratch room for the h8 GEMM's widened weights of smaller projections.
+size_t attention_workspace_max(int cus) { return (size_t)std::max(cus, 1) * 384 * (128 + 4) * sizeof(float); }
 
 namespace {
 
@@ -898,10 +561,12 @@ int launch_attention(const Pipeline &pl, const Exec &ex, const Arg *args, int na
   const uint64_t qx = (uint64_t)(p.H - 1) * p.q_rows + p.Lq, kx = (uint64_t)(p.KVH - 1) * p.k_rows + p.L;
   if (!fits(0, qx * D * es, "q") || !fits(1, kx * D * es, "k") || !fits(2, kx * D * 2, "v")) return -1;
   if (qk8 && (!fits(5, qx * 4, "q_scale") || !fits(6, kx * 4, "k_scale"))) return -1;
-  // the wave-pipelined kernel: D = 128 without a causal mask (unless GROUPS selects an older kernel)
+  // D = 128 without a causal mask: the paired kernel (int8 scores) or the wave-pipelined one (ival[2] = 2 / 1),
+  // unless GROUPS=2 selected this file's kernel (ival[2] = 0)
   constexpr bool CANW = !CAUSAL && D == 128;
-  const bool usew = CANW && pl.ival[2];
-  // the wave kernel addresses a head's K/V rows (and the blocks its pipeline stages past the end) with 32-bit
+  const bool usew = CANW && pl.ival[2] != 0;
+  const bool usep = usew && QKT == T_I8 && pl.ival[2] == 2;
+  // those kernels address a head's K/V rows (and the blocks their pipelines stage past the end) with 32-bit
   // byte offsets
   if (usew && (uint64_t)(p.L + 4 * BK) * D * 2 > 0xffffffffull) {
     *err = "L = " + std::to_string(p.L) + " keys: too long for 32-bit K/V row offsets";
@@ -938,10 +603,7 @@ int launch_attention(const Pipeline &pl, const Exec &ex, const Arg *args, int na
     return -1;
   }
   if (p.Lq == 0) return 0;
-  // int8 scores, D = 128, no causal mask: the three-group kernel (unless GROUPS=2)
-  constexpr bool CAN3 = QKT == T_I8 && !CAUSAL && D == 128;
-  const bool use3 = !usew && CAN3 && pl.ival[1];
-  const int BQ = usew ? WAVE_BQ : use3 ? Cfg3::BQ : C::BQ;
+  const int BQ = usep ? PAIR_BQ : usew ? WAVE_BQ : C::BQ;
   const int nqb = (p.Lq + BQ - 1) / BQ;
   const long ntiles = (long)nqb * p.H;
   if (ntiles > 0x7fffffffL / 256) {
@@ -951,7 +613,7 @@ int launch_attention(const Pipeline &pl, const Exec &ex, const Arg *args, int na
   // Tail split (not for causal masks, whose tiles differ in length, nor for the scores dump): the R tiles of a
   // last, partly filled round of CUs become R * s key chunks, s <= CUs / R, each at least 2 key blocks.
   Split sp{(int)ntiles, 0, 0, nullptr, 0};
-  if (usew) sp.rnd = cu_count() / 8;  // the wave kernel alternates its key order between rounds of an XCD
+  if (usew) sp.rnd = cu_count() / 8;  // these kernels alternate their key order between rounds of an XCD
   const int cus = pl.ival[0] ? cu_count() : 0;
   const int kblocks = (p.L + BK - 1) / BK;
   if (!CAUSAL && (!DUMP || usew) && cus > 0) {
@@ -972,29 +634,8 @@ int launch_attention(const Pipeline &pl, const Exec &ex, const Arg *args, int na
   // the scores hook of the older kernels writes the scores instead of the output
   char *out = DUMP && !usew ? args[7].ptr : args[3].ptr;
   if constexpr (CANW) {
+    if (usep) return launch_attention_pair(VT, OT, DUMP, ex, args, p, nqb, sp, err);
     if (usew) return launch_attention_wave(QKT, VT, OT, DUMP, ex, args, p, nqb, sp, err);
-  }
-  if constexpr (CAN3) {
-    if (use3) {
-      auto kern3 = attention3_kernel<VT, OT, DUMP>;
-      static bool attr3_set = false;
-      if (!attr3_set) {
-        hipError_t e = hipFuncSetAttribute((const void *)kern3, hipFuncAttributeMaxDynamicSharedMemorySize, Cfg3::LDS);
-        if (e != hipSuccess) {
-          *err = std::string("hipFuncSetAttribute: ") + hipGetErrorString(e);
-          return -1;
-        }
-        attr3_set = true;
-      }
-      hipLaunchKernelGGL(kern3, dim3((unsigned)ngroups), dim3(Cfg3::NT), Cfg3::LDS, ex.stream, args[0].ptr, args[1].ptr,
-                         args[2].ptr, out, (const float *)args[5].ptr, (const float *)args[6].ptr, p, nqb, sp);
-      if (sp.s) {
-        const int rows = (int)(ntiles - sp.nfull) * Cfg3::BQ;
-        hipLaunchKernelGGL((attention_merge<D, OT, Cfg3::BQ>), dim3((unsigned)(rows / 4)), dim3(256), 0, ex.stream, sp.ws,
-                           args[3].ptr, p, nqb, sp.nfull, sp.s);
-      }
-      return 0;
-    }
   }
   auto kern = attention_kernel<D, QKT, VT, OT, CAUSAL, DUMP>;
   static bool attr_set = false;
@@ -1056,9 +697,10 @@ int type_of(const std::string &s) {
 // as integers and do not change the gfx950 kernel (its tiles are its own).
 // SPLIT (this build's, default 1): allow the tail split of a partly filled
 // last round of workgroups; SPLIT=0 runs every tile whole. GROUPS (this
-// build's, default 1): HD 128 without a causal mask runs on the wave-pipelined
-// kernel; GROUPS=3 selects the three-group kernel (int8 scores) and GROUPS=2 the
-// two-group (ping-pong) one, which also serves every other case.
+// build's, default 0): HD 128 without a causal mask runs on the paired kernel
+// with int8 scores and on the wave-pipelined kernel with 16-bit scores;
+// GROUPS=1 selects the wave-pipelined kernel, GROUPS=2 the two-group (ping-pong)
+// one, which also serves every other case, and GROUPS=3 the paired kernel.
 bool make_attention(const std::string &fn, const Macros &m, Pipeline *pl, std::string *err) {
   const bool dump = fn == "attention_scores";
   if (fn != "attention" && !dump) {
@@ -1072,9 +714,13 @@ bool make_attention(const std::string &fn, const Macros &m, Pipeline *pl, std::s
   for (const char *k : {"WM", "BK", "KPAD", "DB", "PVORDER", "VX", "SLACK", "TG"})
     if (!macro_int(m, k, 0, &dummy, err)) return false;
   int split, groups;
-  if (!macro_int(m, "SPLIT", 1, &split, err) || !macro_int(m, "GROUPS", 1, &groups, err)) return false;
-  if (groups < 1 || groups > 3) {
-    *err = "GROUPS must be 1, 2 or 3";
+  if (!macro_int(m, "SPLIT", 1, &split, err) || !macro_int(m, "GROUPS", 0, &groups, err)) return false;
+  if (groups < 0 || groups > 3) {
+    *err = "GROUPS must be 0 (default), 1, 2 or 3";
+    return false;
+  }
+  if (groups == 3 && !qk8) {
+    *err = "GROUPS=3 (the paired kernel) needs int8 scores (QK8=1)";
     return false;
   }
   for (auto &kv : m) {
@@ -1103,12 +749,13 @@ bool make_attention(const std::string &fn, const Macros &m, Pipeline *pl, std::s
   else if (hd == 96) f = dump ? pick_types<96, true>(qkt, it, ot, causal) : pick_types<96, false>(qkt, it, ot, causal);
   else f = dump ? pick_types<64, true>(qkt, it, ot, causal) : pick_types<64, false>(qkt, it, ot, causal);
   pl->launch = f;
-  // workgroup size of the kernel the pipeline launches (the three-group kernel: int8, HD 128, no causal mask)
-  const bool wave = groups == 1 && hd == 128 && !causal;
-  pl->threads = wave ? WAVE_THREADS : (groups == 3 && qk8 && hd == 128 && !causal) ? NW3 * 64 : NW * 64;
+  // the kernel the pipeline launches for HD 128 without a causal mask: 2 the paired kernel (int8 scores), 1 the
+  // wave-pipelined kernel, 0 this file's two-group kernel (which serves every other case)
+  int ksel = 0;
+  if (hd == 128 && !causal) ksel = groups == 0 ? (qk8 ? 2 : 1) : groups == 1 ? 1 : groups == 3 ? 2 : 0;
+  pl->threads = ksel == 2 ? PAIR_THREADS : ksel == 1 ? WAVE_THREADS : NW * 64;
   pl->ival[0] = split != 0;
-  pl->ival[1] = groups == 3;
-  pl->ival[2] = wave;
+  pl->ival[2] = ksel;
   return true;
 }
 

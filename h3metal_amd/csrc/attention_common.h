@@ -36,6 +36,12 @@ constexpr int WAVE_BQ = 128 * WAVE_NU;  // query rows per workgroup of the wave-
 constexpr int WAVE_THREADS = 256;       // its workgroup: 4 waves, one per SIMD
 int launch_attention_wave(int qkt, int vt, int ot, bool dump, const Exec &ex, const Arg *args, const AttnParams &p,
                           int nqb, const Split &sp, std::string *err);
+// The paired kernel (attention_pair.hip): int8 scores, D = 128 without a causal mask, 8 waves (two per SIMD) over
+// PAIR_BQ query rows; vt, ot as above.
+constexpr int PAIR_BQ = 256;
+constexpr int PAIR_THREADS = 512;
+int launch_attention_pair(int vt, int ot, bool dump, const Exec &ex, const Arg *args, const AttnParams &p, int nqb,
+                          const Split &sp, std::string *err);
 
 
 namespace {

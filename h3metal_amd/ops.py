@@ -66,8 +66,9 @@ def attention_scores(gpu: Gpu, q: Tensor, k: Tensor, v: Tensor, scores: Tensor, 
     """Test hook (no reference counterpart): attention as ops.attention runs it, plus the raw score accumulators
     of its MFMAs, scores[h][i][j] = q_i . k_j (int32 for int8 inputs, f32 otherwise) for keys j < L. At D = 128
     without a causal mask the kernel that runs is ops.attention's own (same tiles, staging, tail split and
-    P V), which then also writes `out` ([Lq][H * D] rows, as ops.attention with seq_heads = H). GROUPS=2 / 3
-    select the older kernels, which write the scores only."""
+    P V), which then also writes `out` ([Lq][H * D] rows, as ops.attention with seq_heads = H). GROUPS=1 / 3
+    select the wave-pipelined / paired kernel the same way; GROUPS=2 the two-group kernel, which writes the
+    scores only."""
     q8 = q_scale is not None
     vt = v.dtype if v.dtype in ("f16", "bf16") else "bf16"
     if out is None:

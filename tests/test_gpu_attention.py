@@ -62,8 +62,9 @@ def run_attention(gpu, q, k, v, *, dtype, Lq, L, H, KVH, D, scale, causal=False,
 @pytest.mark.parametrize("Lq,L,H,KVH,D", [(100, 100, 2, 2, 128), (77, 300, 3, 3, 128), (64, 64, 4, 1, 64),
                                           (300, 1037, 2, 1, 128), (1, 5, 1, 1, 128), (700, 449, 2, 2, 128)])
 def test_int32_scores_bit_exact(gpu, Lq, L, H, KVH, D, groups):
-    """int32 score accumulators of the kernel that runs (int8, D=128: the wave-pipelined kernel; GROUPS=3 / 2 the
-    older three- and two-group kernels; D=64 always the two-group one) equal the exact integer products."""
+    """int32 score accumulators of the kernel that runs equal the exact integer products (int8, D=128: GROUPS=1 the
+    wave-pipelined kernel, 3 the paired kernel (the default), 2 the two-group kernel; D=64 always the two-group
+    one)."""
     rng = np.random.default_rng(Lq + L)
     qi = rng.integers(-127, 128, (H, Lq, D)).astype(np.int8)
     ki = rng.integers(-127, 128, (KVH, L, D)).astype(np.int8)
@@ -564,12 +565,12 @@ def test_tail_split_matches_whole_tiles(gpu, q8_path):
 
 
 @pytest.mark.parametrize("H,KVH,Lq,L,seq", [(4, 4, 1000, 1500, None), (6, 2, 777, 2049, None), (4, 4, 300, 700, 2)])
-def test_int8_three_group_kernel_matches_ping_pong(gpu, H, KVH, Lq, L, seq):
-    """int8 scores at D=128 without a causal mask run on the wave-pipelined kernel (GROUPS=1, the default);
-    GROUPS=3 / 2 select the three-group and two-group ping-pong kernels. Same inputs through all, with and
-    without the tail split:
-    every output meets the tolerance against float64 and the kernels agree to rounding. Ragged L (a partly masked
-    last key block), GQA, several 384-row query blocks per head and batched sequences (seq_heads) included."""
+def test_int8_paired_kernel_matches_other_kernels(gpu, H, KVH, Lq, L, seq):
+    """int8 scores at D=128 without a causal mask run on the paired kernel (two waves per SIMD; the default, and
+    GROUPS=3); GROUPS=1 / 2 select the wave-pipelined and two-group ping-pong kernels. Same inputs through all,
+    with and without the tail split: every output meets the tolerance against float64 and the kernels agree to
+    rounding. Ragged L (a partly masked last key block), GQA, several 256-row query blocks per head and batched
+    sequences (seq_heads) included."""
     rng = np.random.default_rng(H * 1000 + L)
     D = 128
     qr, kr = -(-Lq // 512) * 512, -(-L // 64) * 64 + 64
@@ -581,7 +582,7 @@ def test_int8_three_group_kernel_matches_ping_pong(gpu, H, KVH, Lq, L, seq):
     seq_heads = seq or H
     nseq = H // seq_heads
     outs = []
-    for groups, split in ((1, 1), (1, 0), (3, 1), (3, 0), (2, 1)):
+    for groups, split in ((0, 1), (3, 0), (1, 1), (1, 0), (2, 1)):
         print(f"[attention] groups={groups} split={split} H={H} KVH={KVH} Lq={Lq} L={L} seq={seq}", flush=True)
         O = gpu.empty((nseq * qr, seq_heads * D), "f32")
         ops.attention(gpu, Q, K, V, O, Lq=Lq, L=L, H=H, KVH=KVH, D=D, q_rows=qr, k_rows=kr, scale=D ** -0.5,
@@ -600,19 +601,23 @@ def test_int8_three_group_kernel_matches_ping_pong(gpu, H, KVH, Lq, L, seq):
 
 
 def test_groups_macro_refused(gpu):
-    """GROUPS accepts 1, 2 or 3 only (checked on the host when the pipeline is made)."""
+    """GROUPS accepts 0 to 3 only, and 3 (the paired kernel) only with int8 scores (checked on the host when the
+    pipeline is made)."""
     from h3metal_amd.gpu import GpuError
     with pytest.raises(GpuError, match="GROUPS"):
         gpu.kernel("attention", "attention", HD=128, QK8=1, IN_T="bfloat", O_T="bfloat", GROUPS=4)
+    with pytest.raises(GpuError, match="GROUPS=3"):
+        gpu.kernel("attention", "attention", HD=128, QK8=0, IN_T="bfloat", O_T="bfloat", GROUPS=3)
 
 
-@pytest.mark.parametrize("Lq,L", [(1, 1), (5, 63), (384, 64), (385, 65), (17, 129), (700, 191)])
+@pytest.mark.parametrize("Lq,L", [(1, 1), (5, 63), (384, 64), (385, 65), (17, 129), (700, 191), (64, 31), (65, 33),
+                                  (257, 97), (200, 160)])
 @pytest.mark.parametrize("groups", [1, 3])
-def test_int8_three_group_kernel_edges(gpu, Lq, L, groups):
-    """Edge shapes through the wave-pipelined (GROUPS=1) and three-group kernels (int8, D=128, no causal mask):
-    one query or one key, key counts around the 64-key block (the last block's rows past L load as zeros and are
-    masked), query counts around the 256- and 384-row tiles. Checked against float64 within the north-star
-    tolerance."""
+def test_int8_kernel_edges(gpu, Lq, L, groups):
+    """Edge shapes through the wave-pipelined (GROUPS=1) and paired kernels (GROUPS=3; int8, D=128, no causal
+    mask): one query or one key, key counts around the 64-key block and the 32-key halves of the paired kernel
+    (the last block's rows past L load as zeros and are masked), query counts around the 64-row pairs and the
+    256-row tiles. Checked against float64 within the north-star tolerance."""
     rng = np.random.default_rng(Lq * 1000 + L)
     H, D = 2, 128
     qr, kr = -(-Lq // 384) * 384, -(-L // 64) * 64
