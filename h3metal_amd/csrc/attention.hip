@@ -46,12 +46,11 @@
 //    LDS at the end of its second half-step.
 //  * The 1-D grid is remapped so that each XCD (own L2) runs a contiguous
 //    range of (head, query-block) tiles, which then share one head's K/V in L2.
-//  * D = 128 without a causal mask (the DiT path) runs on other kernels by
-//    default: int8 scores on the paired kernel of attention_pair.hip (two waves
-//    per SIMD), 16-bit scores on the wave-pipelined kernel of
-//    attention_wave.hip. The macro GROUPS selects a kernel for A/B tests:
-//    1 the wave-pipelined one, 2 this file's two-group kernel, 3 the paired one
-//    (int8 scores only).
+//  * D = 128 without a causal mask (the DiT path) runs on the wave-pipelined
+//    kernel of attention_wave.hip by default. The macro GROUPS selects a kernel
+//    for A/B tests: 1 the wave-pipelined one, 2 this file's two-group kernel,
+//    3 the paired kernel of attention_pair.hip (two waves per SIMD; int8 scores
+//    only).
 #include "attention_common.h"
 
 #include <algorithm>
@@ -697,10 +696,9 @@ int type_of(const std::string &s) {
 // as integers and do not change the gfx950 kernel (its tiles are its own).
 // SPLIT (this build's, default 1): allow the tail split of a partly filled
 // last round of workgroups; SPLIT=0 runs every tile whole. GROUPS (this
-// build's, default 0): HD 128 without a causal mask runs on the paired kernel
-// with int8 scores and on the wave-pipelined kernel with 16-bit scores;
-// GROUPS=1 selects the wave-pipelined kernel, GROUPS=2 the two-group (ping-pong)
-// one, which also serves every other case, and GROUPS=3 the paired kernel.
+// build's, default 0 = 1): HD 128 without a causal mask runs on the
+// wave-pipelined kernel; GROUPS=2 selects the two-group (ping-pong) kernel,
+// which also serves every other case, and GROUPS=3 the paired kernel (int8).
 bool make_attention(const std::string &fn, const Macros &m, Pipeline *pl, std::string *err) {
   const bool dump = fn == "attention_scores";
   if (fn != "attention" && !dump) {
@@ -749,10 +747,10 @@ bool make_attention(const std::string &fn, const Macros &m, Pipeline *pl, std::s
   else if (hd == 96) f = dump ? pick_types<96, true>(qkt, it, ot, causal) : pick_types<96, false>(qkt, it, ot, causal);
   else f = dump ? pick_types<64, true>(qkt, it, ot, causal) : pick_types<64, false>(qkt, it, ot, causal);
   pl->launch = f;
-  // the kernel the pipeline launches for HD 128 without a causal mask: 2 the paired kernel (int8 scores), 1 the
-  // wave-pipelined kernel, 0 this file's two-group kernel (which serves every other case)
+  // the kernel the pipeline launches for HD 128 without a causal mask: 1 the wave-pipelined kernel (the default),
+  // 2 the paired kernel (int8 scores), 0 this file's two-group kernel (which serves every other case)
   int ksel = 0;
-  if (hd == 128 && !causal) ksel = groups == 0 ? (qk8 ? 2 : 1) : groups == 1 ? 1 : groups == 3 ? 2 : 0;
+  if (hd == 128 && !causal) ksel = groups == 0 || groups == 1 ? 1 : groups == 3 ? 2 : 0;
   pl->threads = ksel == 2 ? PAIR_THREADS : ksel == 1 ? WAVE_THREADS : NW * 64;
   pl->ival[0] = split != 0;
   pl->ival[2] = ksel;

@@ -63,7 +63,7 @@ def run_attention(gpu, q, k, v, *, dtype, Lq, L, H, KVH, D, scale, causal=False,
                                           (300, 1037, 2, 1, 128), (1, 5, 1, 1, 128), (700, 449, 2, 2, 128)])
 def test_int32_scores_bit_exact(gpu, Lq, L, H, KVH, D, groups):
     """int32 score accumulators of the kernel that runs equal the exact integer products (int8, D=128: GROUPS=1 the
-    wave-pipelined kernel, 3 the paired kernel (the default), 2 the two-group kernel; D=64 always the two-group
+    wave-pipelined kernel (the default), 3 the paired kernel, 2 the two-group kernel; D=64 always the two-group
     one)."""
     rng = np.random.default_rng(Lq + L)
     qi = rng.integers(-127, 128, (H, Lq, D)).astype(np.int8)
@@ -566,8 +566,8 @@ def test_tail_split_matches_whole_tiles(gpu, q8_path):
 
 @pytest.mark.parametrize("H,KVH,Lq,L,seq", [(4, 4, 1000, 1500, None), (6, 2, 777, 2049, None), (4, 4, 300, 700, 2)])
 def test_int8_paired_kernel_matches_other_kernels(gpu, H, KVH, Lq, L, seq):
-    """int8 scores at D=128 without a causal mask run on the paired kernel (two waves per SIMD; the default, and
-    GROUPS=3); GROUPS=1 / 2 select the wave-pipelined and two-group ping-pong kernels. Same inputs through all,
+    """int8 scores at D=128 without a causal mask run on the wave-pipelined kernel by default (GROUPS=0 / 1);
+    GROUPS=3 / 2 select the paired (two waves per SIMD) and two-group ping-pong kernels. Same inputs through all,
     with and without the tail split: every output meets the tolerance against float64 and the kernels agree to
     rounding. Ragged L (a partly masked last key block), GQA, several 256-row query blocks per head and batched
     sequences (seq_heads) included."""

@@ -41,8 +41,8 @@ def test_unknown_kernel_and_macros(gpu):
         gpu.kernel("ops", "qk_norm_rope", QKROT=1)
     # the reference's file names and tuning macros are accepted
     k = gpu.kernel("attention.metal", "attention", HD=128, WM=10, BK=32, DB=1, PVORDER=1, VX=1, QK8=1, O_T="bfloat")
-    assert k.max_threads == 512  # the paired kernel's workgroup (int8 scores)
-    assert gpu.kernel("attention", "attention", HD=128, O_T="bfloat").max_threads == 256  # wave-pipelined (16-bit)
+    assert k.max_threads == 256  # the wave-pipelined kernel's workgroup
+    assert gpu.kernel("attention", "attention", HD=128, O_T="bfloat").max_threads == 256
     assert gpu.kernel("attention", "attention", HD=128, QK8=1, O_T="bfloat", GROUPS=1).max_threads == 256
     assert gpu.kernel("attention", "attention", HD=128, QK8=1, O_T="bfloat", GROUPS=3).max_threads == 512
     assert gpu.kernel("attention", "attention", HD=128, QK8=1, O_T="bfloat", GROUPS=2).max_threads == 512
