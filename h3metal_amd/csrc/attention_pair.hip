@@ -322,7 +322,10 @@ __device__ __attribute__((noinline)) void pair_body(const char *Q_, const char *
     float tot[2];
     // The two waves of a pair share a SIMD (waves w and w + 4) and run the step's three independent parts in
     // opposite orders, so that one is in its MFMA-heavy half (16 P V MFMAs) while the other is in its VALU-heavy
-    // half (the softmax and the 8 score MFMAs).
+    // half (the softmax and the 8 score MFMAs). The wave in its softmax half runs at the higher priority: the
+    // SIMD otherwise issues from the older wave first (role 0), which then finishes its step early and waits at
+    // the barrier while role 1, fed only the leftover issue slots, catches up (measured with s_memtime: 2130 vs
+    // 3130 ticks per step in the same code), and MFMAs, long and rarely issued, fill the softmax wave's gaps.
     auto seq = [&]() {
       // 16-key steps of the block in P V order: this wave's two, then its partner's
       constexpr int SS[4] = {2 * R, 2 * R + 1, 2 - 2 * R, 3 - 2 * R};
@@ -381,6 +384,7 @@ __device__ __attribute__((noinline)) void pair_body(const char *Q_, const char *
 #define SB __builtin_amdgcn_sched_barrier(0)
       if constexpr (R == 0) {
         // P V of block j - 1 first (own P from registers), then the softmax of block j and the scores of j + 1
+        __builtin_amdgcn_s_setprio(0);
         VR(0); VR(1); C4(0); C4(1); SB;
         PV(0); VR(2); ST(0); SB;
         PV(1); MU(0, 0); SB;
@@ -398,6 +402,7 @@ __device__ __attribute__((noinline)) void pair_body(const char *Q_, const char *
         PV(13); EX(0, 1); SB;
         PV(14); EX(1, 0); C4(2); C4(3); SB;
         PV(15); EX(1, 1); SB;
+        __builtin_amdgcn_s_setprio(1);
         PK(0, 0); PK(0, 1); MU(2, 0); MU(2, 1); KR(0); KR(1); SB;
         PK(1, 0); PK(1, 1); MU(3, 0); MU(3, 1); pwrite(j, 0); KR(2); KR(3); SB;
         SM(0, 0); FM(2, 0); FM(2, 1); K4(0); K4(1); SB;
@@ -410,6 +415,7 @@ __device__ __attribute__((noinline)) void pair_body(const char *Q_, const char *
         SM(3, 1); PK(3, 0); PK(3, 1); pwrite(j, 1); SB;
       } else {
         // the softmax of block j and the scores of j + 1 first, then P V of block j - 1 (own P read back from LDS)
+        __builtin_amdgcn_s_setprio(1);
         C4(0); C4(1); MU(0, 0); MU(0, 1); SB;
         MU(1, 0); MU(1, 1); FM(0, 0); FM(0, 1); ST(0); SB;
         FM(1, 0); FM(1, 1); EX(0, 0); EX(0, 1); KR(0); KR(1); SB;
@@ -424,6 +430,7 @@ __device__ __attribute__((noinline)) void pair_body(const char *Q_, const char *
         SM(2, 1); EX(3, 1); PO(0, 0); PO(1, 0); SB;
         SM(3, 0); PK(2, 0); PK(2, 1); VR(2); SB;
         SM(3, 1); PK(3, 0); PK(3, 1); pwrite(j, 1); ST(3); SB;
+        __builtin_amdgcn_s_setprio(0);
         PV(0); VR(3); SB;
         PV(1); PO(0, 1); PO(1, 1); SB;
         PV(2); VR(4); SB;
