@@ -34,8 +34,8 @@ PER_FILE = {
     "attention_wave.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"],
     "attention_pair.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"],
 }
-# sources whose inline-assembly MFMAs are checked for hazards in the generated code (isa_check.py)
-ISA_CHECKED = ["attention_wave.hip", "attention_pair.hip"]
+# sources whose inline assembly (MFMAs, DPP fmacs) is checked for hazards in the generated code (isa_check.py)
+ISA_CHECKED = ["attention_wave.hip", "attention_pair.hip", "qk_prepass.hip", "rot_q8.hip"]
 # Kernels with two waves per SIMD (amdgpu-waves-per-eu "2,2") get 256 registers per lane, which the backend splits
 # into equal VGPR and AGPR halves by default. These sources have their device code generated from patched IR
 # instead, with the AGPR share given here (the kernels keep 96 accumulation registers: O and Q), so that the

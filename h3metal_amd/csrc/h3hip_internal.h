@@ -108,34 +108,47 @@ __device__ __forceinline__ float xshfl(float v) {
   else return __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(x, 0x1F | (S << 10)));
 }
 
+// v[i] += c * (v[i] of the lane selected by the DPP control CTRL), for all N values (N even), as assembly: the
+// compiler keeps a separate DPP move for the builtin form. A DPP read needs two wait states after a VALU write of
+// its source; each assembly statement starts with its own s_nop 1 before its (at most eight) reads, so nothing the
+// compiler schedules can come between the wait and the reads, and the statement writes only its own values.
+#define H3_DPP_FMAC_STAGE(CTRL)                                                                                   \
+  do {                                                                                                            \
+    static_assert(N % 2 == 0, "an even number of values per lane");                                             \
+    _Pragma("unroll") for (int i = 0; i + 8 <= N; i += 8) asm volatile(                                          \
+        "s_nop 1\n\tv_fmac_f32_dpp %0, %0, %8 " CTRL "\n\tv_fmac_f32_dpp %1, %1, %8 " CTRL                       \
+        "\n\tv_fmac_f32_dpp %2, %2, %8 " CTRL "\n\tv_fmac_f32_dpp %3, %3, %8 " CTRL                                \
+        "\n\tv_fmac_f32_dpp %4, %4, %8 " CTRL "\n\tv_fmac_f32_dpp %5, %5, %8 " CTRL                                \
+        "\n\tv_fmac_f32_dpp %6, %6, %8 " CTRL "\n\tv_fmac_f32_dpp %7, %7, %8 " CTRL                                \
+        : "+v"(v[i]), "+v"(v[i + 1]), "+v"(v[i + 2]), "+v"(v[i + 3]), "+v"(v[i + 4]), "+v"(v[i + 5]),           \
+          "+v"(v[i + 6]), "+v"(v[i + 7])                                                                         \
+        : "v"(c));                                                                                                \
+    if constexpr (N % 8 >= 4) asm volatile(                                                                       \
+        "s_nop 1\n\tv_fmac_f32_dpp %0, %0, %4 " CTRL "\n\tv_fmac_f32_dpp %1, %1, %4 " CTRL                       \
+        "\n\tv_fmac_f32_dpp %2, %2, %4 " CTRL "\n\tv_fmac_f32_dpp %3, %3, %4 " CTRL                                \
+        : "+v"(v[N / 8 * 8]), "+v"(v[N / 8 * 8 + 1]), "+v"(v[N / 8 * 8 + 2]), "+v"(v[N / 8 * 8 + 3])             \
+        : "v"(c));                                                                                                \
+    if constexpr (N % 4 == 2)                                                                                     \
+      asm volatile("s_nop 1\n\tv_fmac_f32_dpp %0, %0, %2 " CTRL "\n\tv_fmac_f32_dpp %1, %1, %2 " CTRL             \
+                   : "+v"(v[N - 2]), "+v"(v[N - 1])                                                              \
+                   : "v"(c));                                                                                     \
+  } while (0)
+
 // One cross-lane stage of a Walsh-Hadamard transform over lane bit LS, on N values per lane: every lane
 // computes own + c * partner with c = +1 on the lower lane of a pair and -1 on the upper one. The lower lane gets
 // a + b, the upper b - a = -(a - b); partners share every other lane bit, so after stages over a set of lane bits
 // a lane holds its true values times (-1)^(number of those bits set in the lane id), which the caller folds into
 // its final scale (an exact sign change). The product with c is exact and the one rounding is that of the sum,
 // the same as for a + b or a - b (rounding is sign-symmetric). For LS = 1, 2, 8 the shuffled value is the
-// multiplicand of an fmac that reads it straight through DPP (written as assembly, since the compiler keeps a
-// separate DPP move); the leading s_nop gives each DPP read the two wait states it needs after the VALU write
-// of its source, and within a stage each value was written N instructions earlier.
+// multiplicand of an fmac that reads it straight through DPP (H3_DPP_FMAC_STAGE).
 template <int LS, int N>
 __device__ __forceinline__ void hadamard_lane_stage(float (&v)[N], float c) {
-  if constexpr (LS == 1 || LS == 2 || LS == 8) {
-    asm volatile("s_nop 1");
-#pragma unroll
-    for (int i = 0; i < N; i++) {
-      if constexpr (LS == 1)
-        asm volatile("v_fmac_f32_dpp %0, %0, %1 quad_perm:[1,0,3,2] row_mask:0xf bank_mask:0xf bound_ctrl:1"
-                     : "+v"(v[i])
-                     : "v"(c));
-      else if constexpr (LS == 2)
-        asm volatile("v_fmac_f32_dpp %0, %0, %1 quad_perm:[2,3,0,1] row_mask:0xf bank_mask:0xf bound_ctrl:1"
-                     : "+v"(v[i])
-                     : "v"(c));
-      else
-        asm volatile("v_fmac_f32_dpp %0, %0, %1 row_ror:8 row_mask:0xf bank_mask:0xf bound_ctrl:1"
-                     : "+v"(v[i])
-                     : "v"(c));
-    }
+  if constexpr (LS == 1) {
+    H3_DPP_FMAC_STAGE("quad_perm:[1,0,3,2] row_mask:0xf bank_mask:0xf bound_ctrl:1");
+  } else if constexpr (LS == 2) {
+    H3_DPP_FMAC_STAGE("quad_perm:[2,3,0,1] row_mask:0xf bank_mask:0xf bound_ctrl:1");
+  } else if constexpr (LS == 8) {
+    H3_DPP_FMAC_STAGE("row_ror:8 row_mask:0xf bank_mask:0xf bound_ctrl:1");
   } else {
 #pragma unroll
     for (int i = 0; i < N; i++) v[i] = __builtin_fmaf(xshfl<LS>(v[i]), c, v[i]);

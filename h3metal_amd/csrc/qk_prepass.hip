@@ -95,12 +95,7 @@ __device__ __forceinline__ float gshfl(float v) {
 template <int LPS, int B, int N>
 __device__ __forceinline__ void group_stage(float (&v)[N], float c) {
   if constexpr (LPS == 16 && B == 4) {
-    asm volatile("s_nop 1");
-#pragma unroll
-    for (int i = 0; i < N; i++)
-      asm volatile("v_fmac_f32_dpp %0, %0, %1 row_half_mirror row_mask:0xf bank_mask:0xf bound_ctrl:1"
-                   : "+v"(v[i])
-                   : "v"(c));
+    H3_DPP_FMAC_STAGE("row_half_mirror row_mask:0xf bank_mask:0xf bound_ctrl:1");
   } else {
     hadamard_lane_stage<B>(v, c);
   }

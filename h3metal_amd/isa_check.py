@@ -5,10 +5,12 @@ cannot see there (its own builtin MFMAs it protects itself):
   within 18 wait states after it (a 16-pass XDL result is written that late; reading earlier sees the old
   value, writing earlier is overwritten by it), except an MFMA of the same opcode whose srcC is exactly that
   destination (back-to-back accumulation, which the matrix unit forwards without wait states);
-* a VALU write of a register that an MFMA reads, within 2 wait states before that MFMA.
+* a VALU write of a register that an MFMA reads, within 2 wait states before that MFMA;
+* a VALU write of a register that a DPP instruction reads through its DPP operand (src0), within 2 wait states
+  before it (the cross-lane butterflies of the row kernels are DPP fmacs written as assembly).
 
 The scan is straight-line over each function (a conservative approximation across branches: pending results
-are carried into the next block in layout order). Used by build.py on attention_wave.hip; also runnable as
+are carried into the next block in layout order). Used by build.py on the sources it lists in ISA_CHECKED; also runnable as
 `python -m h3metal_amd.isa_check file.s`.
 """
 
@@ -19,6 +21,7 @@ import sys
 
 XDL_WAIT = 18
 VALU_TO_MFMA = 2
+VALU_TO_DPP = 2
 
 
 def _regs(tok: str) -> set:
@@ -78,6 +81,11 @@ def scan(text: str, name: str = "<asm>") -> list[str]:
                     pending[r] = XDL_WAIT + 1  # reads k + 1 after k wait states: clear once k >= XDL_WAIT
                     asm_dst[r] = (op, args[0])
         elif not op.startswith("s_"):
+            if op.endswith("_dpp") and len(args) > 1:
+                for r in _regs(args[1]):
+                    if r in recent and recent[r] - 1 < VALU_TO_DPP:
+                        problems.append(f"{name}:{ln}: VALU write of {r} {recent[r] - 1} wait states before the DPP "
+                                        f"read: {s}")
             used = set().union(*[_regs(a) for a in args]) if args else set()
             hit = sorted(r for r in used if pending.get(r, 0) > 0)
             if hit:
@@ -92,7 +100,7 @@ def scan(text: str, name: str = "<asm>") -> list[str]:
                 del pending[r]
         for r in list(recent):
             recent[r] += ws
-            if recent[r] > VALU_TO_MFMA + 1:
+            if recent[r] > max(VALU_TO_MFMA, VALU_TO_DPP) + 1:
                 del recent[r]
     return problems
 

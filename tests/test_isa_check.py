@@ -1,4 +1,4 @@
-"""The build-time hazard check of inline-assembly MFMAs (h3metal_amd/isa_check.py) on small hand-written
+"""The build-time hazard check of inline-assembly MFMAs and DPP reads (h3metal_amd/isa_check.py) on small hand-written
 assembly listings: each hazard it exists for is reported, and the patterns it must accept (enough wait states,
 back-to-back accumulation onto the same registers) are not."""
 
@@ -54,3 +54,19 @@ def test_valu_write_just_before_an_mfma_operand_is_reported():
 
 def test_a_new_function_starts_clean():
     assert scan(listing(ASM_MFMA) + "\nother_kern:\nv_accvgpr_read_b32 v8, a3") == []
+
+
+def test_valu_write_just_before_a_dpp_read_is_reported():
+    w = "v_fmac_f32_e32 v1, v2, v3"
+    dpp = "v_fmac_f32_dpp v1, v1, v9 quad_perm:[1,0,3,2] row_mask:0xf bank_mask:0xf bound_ctrl:1"
+    assert len(scan(listing(w, dpp))) == 1
+    assert len(scan(listing(w, "s_nop 0", dpp))) == 1
+    assert scan(listing(w, "s_nop 1", dpp)) == []
+    # two independent instructions in between are two wait states as well
+    assert scan(listing(w, "v_add_f32 v5, v6, v7", "v_add_f32 v5, v6, v7", dpp)) == []
+    # only the DPP operand (src0) counts: the other source may be written just before
+    assert scan(listing("v_mov_b32 v9, 0", dpp)) == []
+    # four DPP fmacs after one s_nop 1, each on its own value (the form the row kernels use)
+    block = ["s_nop 1"] + [f"v_fmac_f32_dpp v{i}, v{i}, v9 row_ror:8 row_mask:0xf bank_mask:0xf bound_ctrl:1"
+                           for i in range(1, 5)]
+    assert scan(listing(*[f"v_add_f32 v{i}, v{i}, v{i}" for i in range(1, 5)], *block)) == []
