@@ -1,7 +1,7 @@
 """Attention throughput on one MI355X: the headline metric (attention TFLOP/s and % of the int8 MFMA peak at
 H=32, D=128, S=16896; ms per call).
 
-    python bench.py [--gpus 1] [--steps 20] [--warmup 10] [--config c4] [--no-cpu]
+    python bench.py [--gpus 1] [--steps 20] [--warmup 10] [--config c4] [--no-cpu] [--extra c2,c3,c5]
 
 A step is one attention call over the whole workload (all heads, all query rows) with its inputs resident in
 HBM. The default workload is benchmark config 4: B=1, H=32, D=128, S=16896 (512 text + 16384 image rows), Q/K bf16
@@ -11,7 +11,9 @@ rot_q8 (256-block Hadamard + per-row int8 of O), is timed on the call's own outp
 the int8 projections around attention (qkv, output) at the config's S and H*D under "gemm_q8". FLOPs follow the reference's
 convention 4*H*Sq*Sk_valid*D (bench/attn_bench.py:27). The timed region is bracketed by stream
 synchronisations; GPU time comes from HIP events on the library's stream (h3_wait), per-launch durations from
-per-dispatch event pairs (profile mode). One JSON line is printed.
+per-dispatch event pairs (profile mode). The other benchmark configs (--extra: configs 2, 3 and 5 by default) are
+timed the same way in the same run and reported as extra keys of the line; the plain-copy yardstick of the
+streaming kernels is the library's own device copy. One JSON line is printed.
 """
 
 from __future__ import annotations
@@ -132,29 +134,52 @@ def cpu_baseline(kw, cfg, L, budget_s=20.0):
                       f"extrapolated x{H} heads = {total:.2f} s per call"}
 
 
-def copy_rates(sizes, reps=10):
-    """Bytes per second of a plain device copy moving the same traffic as each of `sizes` (n / 2 read, n / 2
-    written): the HBM rate a streaming kernel of that size can reach on this part (torch's copy kernel). Run in a
-    child process: torch brings its own HIP runtime, which must not share a process with this library's."""
-    import subprocess
-    code = ("import json, sys, torch\n"
-            "out = []\n"
-            "for nb in json.loads(sys.argv[1]):\n"
-            "    n = nb // 2\n"
-            "    a = torch.ones(n, dtype=torch.uint8, device='cuda'); b = torch.empty_like(a)\n"
-            "    for _ in range(3): b.copy_(a)\n"
-            "    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)\n"
-            f"    e0.record()\n    for _ in range({reps}): b.copy_(a)\n"
-            "    e1.record(); torch.cuda.synchronize()\n"
-            f"    out.append(2 * n / (e0.elapsed_time(e1) / {reps} / 1e3))\n"
-            "    del a, b; torch.cuda.empty_cache()\n"
-            "print(json.dumps(out))\n")
-    try:
-        r = subprocess.run([sys.executable, "-c", code, json.dumps([int(x) for x in sizes])], capture_output=True,
-                           text=True, timeout=300)
-        return json.loads(r.stdout.strip().splitlines()[-1])
-    except Exception:  # noqa: BLE001 -- the yardstick is optional
-        return [None] * len(sizes)
+def copy_rates(gpu, sizes, reps=10):
+    """Bytes per second of a plain device-to-device copy moving the same traffic as each of `sizes` (n / 2 read,
+    n / 2 written), through the library's own copy (h3_buffer_copy on its stream, timed per copy by HIP events):
+    the HBM rate a streaming kernel of that size can reach on this part."""
+    out = []
+    for nb in sizes:
+        n = int(nb) // 2
+        src, dst = gpu.empty((n,), "u8"), gpu.empty((n,), "u8")
+        for _ in range(3):
+            src.copy_to(dst)
+        gpu.wait()
+        gpu.profile(True)
+        for _ in range(reps):
+            src.copy_to(dst)
+        gpu.wait()
+        t = float(np.mean([s for _, s in gpu.profile_take()]))
+        gpu.profile(False)
+        out.append(2 * n / t)
+        del src, dst
+    return out
+
+
+def extra_config(gpu, cfg, steps, warmup):
+    """ms per attention call, TFLOP/s and fraction of the MFMA peak of its score type at one more benchmark config
+    (timed like the headline: HIP events on the library's stream over `steps` calls after `warmup`)."""
+    from h3metal_amd import ops
+    H, D, S, _, path = CONFIGS[cfg]
+    kw, _, L = make_inputs(gpu, cfg, np.random.default_rng(1))
+    O = gpu.empty((S, H * D), "bf16")
+
+    def step():
+        ops.attention(gpu, kw["q"], kw["k"], kw["v"], O, Lq=S, L=L, H=H, KVH=H, D=D, q_rows=S, k_rows=S,
+                      scale=D ** -0.5, q_scale=kw.get("q_scale"), k_scale=kw.get("k_scale"))
+    for _ in range(warmup):
+        step()
+    gpu.wait()
+    for _ in range(steps):
+        step()
+    sec = gpu.wait() / steps
+    flops = 4.0 * H * S * L * D
+    peak = PEAK["int8" if path == "int8" else "bf16"]
+    return {"workload": f"B=1 H={H} D={D} Sq={S} Sk_valid={L}, "
+                        f"{'Hadamard-rotated int8 Q/K + bf16 V' if path == 'int8' else 'bf16 Q/K/V'}",
+            "ms": round(sec * 1e3, 4), "TFLOP/s": round(flops / sec / 1e12, 1),
+            "frac_peak": round(flops / sec / peak, 4), "peak": f"{'int8' if path == 'int8' else 'bf16'} "
+                                                              f"{peak / 1e12:.0f} TFLOP/s", "steps": steps}
 
 
 def traffic(kernel, cfg="c4"):
@@ -180,17 +205,20 @@ def main():
     ap.add_argument("--config", default="c4", choices=sorted(CONFIGS))
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--cpu-budget", type=float, default=20.0)
+    ap.add_argument("--extra", default="c2,c3,c5",
+                    help="other configs timed in the same run and reported as extra keys ('' for none)")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="only run a plain device copy of MIB MiB (to scale rocprofv3 FETCH_SIZE / WRITE_SIZE)")
     args = ap.parse_args()
     CONFIGS_ARG["config"] = args.config
     if args.calibrate_copy:
-        import torch
+        from h3metal_amd.gpu import Gpu
+        gpu = Gpu()
         n = args.calibrate_copy * 2 ** 20
-        a = torch.ones(n, dtype=torch.uint8, device="cuda")
-        b = torch.empty_like(a)
-        b.copy_(a)
-        torch.cuda.synchronize()
+        src, dst = gpu.empty((n,), "u8"), gpu.empty((n,), "u8")
+        src.copy_to(dst)
+        gpu.wait()
+        gpu.close()
         print(json.dumps({"calibrate_copy_bytes": n}))
         return
     if args.gpus != 1:
@@ -298,17 +326,20 @@ def main():
         gl[name] = {"M": S, "N": n_out, "K": dm, "ms": round(gt * 1e3, 4), "TOPS": round(ops_n / gt / 1e12, 1),
                     "frac_int8_peak": round(ops_n / gt / PEAK["int8"], 4)}
     out["gemm_q8"] = gl
-    if not args.no_cpu:
-        out["cpu_baseline"] = cpu_baseline(kw, args.config, L, args.cpu_budget)
-    gpu.close()
-    # the plain-copy HBM rate at the streaming kernels' traffic sizes (measured after this library's context is
-    # closed): what a kernel that only moves these bytes reaches on this part
+    # the plain-copy HBM rate at the streaming kernels' traffic sizes: what a kernel that only moves these bytes
+    # reaches on this part
     for key in ("prepass", "rot_q8"):
         if key in out:
-            cr = copy_rates([out[key]["bytes"]])[0]
-            if cr:
-                out[key]["copy_GB/s"] = round(cr / 1e9, 1)
-                out[key]["frac_copy"] = round(out[key]["GB/s"] * 1e9 / cr, 4)
+            cr = copy_rates(gpu, [out[key]["bytes"]])[0]
+            out[key]["copy_GB/s"] = round(cr / 1e9, 1)
+            out[key]["frac_copy"] = round(out[key]["GB/s"] * 1e9 / cr, 4)
+    if not args.no_cpu:
+        out["cpu_baseline"] = cpu_baseline(kw, args.config, L, args.cpu_budget)
+    # the other benchmark configs, timed in the same run (the headline stays the --config one)
+    del kw, O, A8, QKV, X  # the headline workload's buffers
+    for cfg in [c for c in args.extra.split(",") if c and c != args.config]:
+        out[cfg] = extra_config(gpu, cfg, steps=4 if cfg == "c5" else args.steps, warmup=2 if cfg == "c5" else 5)
+    gpu.close()
     print(json.dumps(out), flush=True)
 
 

@@ -324,6 +324,42 @@ int h3_buffer_read(h3_ctx *ctx, void *buf, uint64_t offset, void *dst, uint64_t 
   return 0;
 }
 
+// Stream work is timed from the first operation after a wait (t0) to the next h3_wait; in profile mode each
+// operation also gets its own pair of events.
+static bool op_begin(h3_ctx *ctx, bool prof, hipEvent_t *e0, hipEvent_t *e1) {
+  if (!ctx->timing) {
+    if (!hip_ok(hipEventRecord(ctx->t0, ctx->stream), "hipEventRecord")) return false;
+    ctx->timing = true;
+  }
+  if (prof && (!hip_ok(hipEventCreate(e0), "hipEventCreate") || !hip_ok(hipEventCreate(e1), "hipEventCreate") ||
+               !hip_ok(hipEventRecord(*e0, ctx->stream), "hipEventRecord")))
+    return false;
+  return true;
+}
+static void op_end(h3_ctx *ctx, hipEvent_t e0, hipEvent_t e1) {
+  if (!e0) return;
+  hipEventRecord(e1, ctx->stream);
+  ctx->prof_events.emplace_back(e0, e1);
+}
+
+int h3_buffer_copy(h3_ctx *ctx, void *dst, uint64_t dst_offset, void *src, uint64_t src_offset, uint64_t bytes) {
+  if (copy_check(ctx, dst, dst_offset, bytes, "h3_buffer_copy (destination)") ||
+      copy_check(ctx, src, src_offset, bytes, "h3_buffer_copy (source)"))
+    return -1;
+  if (!bytes) return 0;
+  hipEvent_t e0 = nullptr, e1 = nullptr;
+  if (!op_begin(ctx, ctx->profile, &e0, &e1)) return -1;
+  char *d = static_cast<char *>(static_cast<Buffer *>(dst)->dev) + dst_offset;
+  const char *sp = static_cast<const char *>(static_cast<Buffer *>(src)->dev) + src_offset;
+  if (!hip_ok(hipMemcpyAsync(d, sp, bytes, hipMemcpyDeviceToDevice, ctx->stream), "hipMemcpyAsync")) {
+    if (e0) hipEventDestroy(e0);
+    if (e1) hipEventDestroy(e1);
+    return -1;
+  }
+  op_end(ctx, e0, e1);
+  return 0;
+}
+
 void *h3_pipeline(h3_ctx *ctx, const char *file, const char *fn, const char *macros) {
   if (!ctx || !file || !fn) {
     set_error("h3_pipeline: missing context, file or function name");
@@ -388,18 +424,9 @@ static int dispatch(h3_ctx *ctx, void *pso, const h3_arg *bufs, int nbufs, const
     args[i].ptr = static_cast<char *>(b->dev) + bufs[i].offset;
     args[i].avail = b->bytes - bufs[i].offset;
   }
-  if (!ctx->timing) {
-    if (!hip_ok(hipEventRecord(ctx->t0, ctx->stream), "hipEventRecord")) return -1;
-    ctx->timing = true;
-  }
   // per-dispatch profiling creates events; the allocation-free entry point does not profile
-  const bool prof = ctx->profile && !no_alloc;
   hipEvent_t e0 = nullptr, e1 = nullptr;
-  if (prof) {
-    if (!hip_ok(hipEventCreate(&e0), "hipEventCreate") || !hip_ok(hipEventCreate(&e1), "hipEventCreate") ||
-        !hip_ok(hipEventRecord(e0, ctx->stream), "hipEventRecord"))
-      return -1;
-  }
+  if (!op_begin(ctx, ctx->profile && !no_alloc, &e0, &e1)) return -1;
   std::string err;
   h3::Exec ex;
   ex.stream = ctx->stream;
@@ -417,10 +444,7 @@ static int dispatch(h3_ctx *ctx, void *pso, const h3_arg *bufs, int nbufs, const
     set_error(pl->name + ": launch failed: " + hipGetErrorString(le));
     return -1;
   }
-  if (prof) {
-    hipEventRecord(e1, ctx->stream);
-    ctx->prof_events.emplace_back(e0, e1);
-  }
+  op_end(ctx, e0, e1);
   return 0;
 }
 

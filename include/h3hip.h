@@ -64,6 +64,10 @@ int h3_buffer_write(h3_ctx *ctx, void *buf, uint64_t offset, const void *src, ui
 int h3_buffer_read(h3_ctx *ctx, void *buf, uint64_t offset, void *dst, uint64_t bytes);
 // The device address of a buffer (for callers that launch their own HIP work).
 void *h3_buffer_device(void *buf);
+// Addition (no reference counterpart; a Metal caller copies through shared memory): copies `bytes` from `src` at
+// `src_offset` to `dst` at `dst_offset` on the context's stream, in order with the dispatches (asynchronous;
+// timed by h3_wait and, in profile mode, recorded like a dispatch). Returns 0, or -1 on a bad range.
+int h3_buffer_copy(h3_ctx *ctx, void *dst, uint64_t dst_offset, void *src, uint64_t src_offset, uint64_t bytes);
 
 // Looks up kernel `fn` of module `file` specialised by macros "NAME=value;...".
 // Modules: "attention" (fn "attention", "attention_scores") and "ops" (fn

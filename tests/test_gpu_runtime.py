@@ -86,6 +86,47 @@ def test_wait_time_and_profile(gpu):
     assert prof[0][0].startswith("attention:attention(")
 
 
+def test_profile_names_with_static_launches_and_copies(gpu):
+    """In profile mode every timed operation (h3_dispatch launches, device copies) gets its name back in order;
+    launches through the allocation-free entry point are not timed and take no name."""
+    H, S, D = 2, 512, 128
+    rng = np.random.default_rng(1)
+    Q = gpu.upload(rng.standard_normal((H, S, D)).astype(np.float16))
+    O = gpu.empty((S, H * D), "f16")
+    C = gpu.empty((S, H * D), "f16")
+    k = gpu.kernel("attention", "attention", HD=D)
+    params = pack("7if3i", S, S, H, H, S, S, H * D, D ** -0.5 * ops.LOG2E, 0, H, 0)
+    gpu.wait()
+    gpu.profile(True)
+    gpu.launch(k, None, None, [Q, Q, Q, O], params)
+    gpu.launch(k, None, None, [Q, Q, Q, O], params, no_alloc=True)
+    O.copy_to(C)
+    gpu.launch(k, None, None, [Q, Q, Q, O], params, no_alloc=True)
+    gpu.launch(k, None, None, [Q, Q, Q, O], params)
+    gpu.wait()
+    prof = gpu.profile_take()
+    gpu.profile(False)
+    assert [n for n, _ in prof] == [k.name, "h3_buffer_copy", k.name]
+    assert all(t > 0 for _, t in prof)
+    assert gpu.names == []
+    assert np.array_equal(C.numpy(), O.numpy())
+
+
+def test_device_copy(gpu):
+    """h3_buffer_copy moves bytes between (views of) device buffers in order with the stream; bad ranges are
+    refused."""
+    from h3metal_amd.gpu import GpuError
+    rng = np.random.default_rng(2)
+    a = rng.integers(0, 255, 10000).astype(np.uint8)
+    A = gpu.upload(a, "u8")
+    B = gpu.empty((12000,), "u8")
+    A.view((5000,), offset_elems=1000).copy_to(B.view((5000,), offset_elems=7000))
+    got = B.numpy()
+    assert np.array_equal(got[7000:12000], a[1000:6000]) and not got[:7000].any()
+    with pytest.raises(GpuError, match="outside"):
+        A.copy_to(B.view((4000,), offset_elems=8000))
+
+
 def test_misaligned_views_refused(gpu):
     """Q/K/V rows are read 16 bytes at a time and O written 4 elements at a time: a view whose base breaks
     that is refused on the host, not run."""

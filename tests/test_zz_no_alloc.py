@@ -62,7 +62,8 @@ def test_static_attention_matches_dispatch(gpu, H, S):
 
 def test_static_h8_gemm(gpu):
     """The h8 GEMM's widened weights live in the static scratch: a product that fits matches h3_dispatch bit for
-    bit, one that needs more than the 32 MiB is refused with the size it needs."""
+    bit; one that needs more than the 32 MiB is refused with the size it needs, although the context's own
+    workspace (grown to 48 MiB) runs it through h3_dispatch."""
     rng = np.random.default_rng(3)
     M, N, K = 64, 256, 512
     a = gpu.upload(rng.standard_normal((M, K)).astype(np.float16))
@@ -75,13 +76,25 @@ def test_static_h8_gemm(gpu):
                    pack("8i", M, n, kk, kk, n, kk, kk // 128, n), params_index=8, no_alloc=no_alloc)
         gpu.wait()
         return out.numpy()
+    ws = gpu.workspace_bytes
     want = run(False, N, K, w, gpu.empty((M, N), "f16"))
     got = run(True, N, K, w, gpu.empty((M, N), "f16"))
     assert np.array_equal(got, want)
-    Nb, Kb = 4096, 8192  # 64 MiB of widened weights
-    wb = gpu.empty((Nb, Kb), "i8")
-    ab = gpu.empty((M, Kb), "f16")
+    # 40 MiB of widened weights: more than the 32 MiB static array, less than a context workspace of 48 MiB. The
+    # ordinary entry point runs it; the allocation-free one refuses it (it never uses the context's workspace).
+    gpu.reserve_workspace(48 << 20)
+    ws = gpu.workspace_bytes
+    assert ws >= 48 << 20
+    Nb, Kb = 4096, 5120
+    wb = gpu.upload(rng.integers(-127, 128, (Nb, Kb)).astype(np.int8), "i8")
+    ab = gpu.upload(rng.standard_normal((M, Kb)).astype(np.float16))
+    swb = gpu.upload(rng.uniform(1e-3, 1e-2, Nb).astype(np.float32))
+    ob = gpu.empty((M, Nb), "f16")
+    bufs = [ab, wb, swb, None, ob, None, None, None]
+    params = pack("8i", M, Nb, Kb, Kb, Nb, Kb, Kb // 128, Nb)
+    gpu.launch(k, None, None, bufs, params, params_index=8)
+    gpu.wait()
+    assert np.isfinite(ob.numpy().astype(np.float32)).all() and np.abs(ob.numpy().astype(np.float32)).max() > 0
     with pytest.raises(GpuError, match="bytes of scratch"):
-        gpu.launch(k, None, None, [ab, wb, gpu.empty((Nb,), "f32"), None, gpu.empty((M, Nb), "f16"), None, None,
-                                   None], pack("8i", M, Nb, Kb, Kb, Nb, Kb, Kb // 128, Nb), params_index=8,
-                   no_alloc=True)
+        gpu.launch(k, None, None, bufs, params, params_index=8, no_alloc=True)
+    assert gpu.workspace_bytes == ws  # the static calls neither used nor grew the context's workspace
