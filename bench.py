@@ -206,7 +206,7 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--cpu-budget", type=float, default=20.0)
     ap.add_argument("--groups", type=int, default=0,
-                    help="attention kernel selector (the GROUPS macro: 0 default, 1 wave-pipelined, 3 paired)")
+                    help="attention kernel selector (the GROUPS macro: 0 default, 1 wave-pipelined, 3 paired, 4 ping-pong)")
     ap.add_argument("--extra", default="c2,c3,c5",
                     help="other configs timed in the same run and reported as extra keys ('' for none)")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",

@@ -26,6 +26,8 @@ LIB = os.path.join(HERE, "libh3hip.so")
 
 COMMON = ["--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC", "-Wall", "-Wno-unused-function",
           "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
+# H3_DEFINES (space-separated -D flags) builds a variant, e.g. the attention kernels' timing-only instrumentation
+COMMON += [f for f in os.environ.get("H3_DEFINES", "").split() if f.startswith("-D")]
 PER_FILE = {
     "qk_prepass.hip": ["-ffp-contract=off"],
     "rot_q8.hip": ["-ffp-contract=off"],
@@ -33,15 +35,16 @@ PER_FILE = {
     # score MFMAs with VGPR results (the softmax reads them), P V accumulators in AGPRs (inline assembly)
     "attention_wave.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"],
     "attention_pair.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"],
+    "attention_pp.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"],
 }
 # sources whose inline assembly (MFMAs, DPP fmacs) is checked for hazards in the generated code (isa_check.py)
-ISA_CHECKED = ["attention_wave.hip", "attention_pair.hip", "qk_prepass.hip", "rot_q8.hip"]
+ISA_CHECKED = ["attention_wave.hip", "attention_pair.hip", "attention_pp.hip", "qk_prepass.hip", "rot_q8.hip"]
 # Kernels with two waves per SIMD (amdgpu-waves-per-eu "2,2") get 256 registers per lane, which the backend splits
 # into equal VGPR and AGPR halves by default. These sources have their device code generated from patched IR
 # instead, with the AGPR share given here (the kernels keep 96 accumulation registers: O and Q), so that the
 # VGPRs of the softmax and the operands get the rest.
-AGPR_ALLOC = {"attention_pair.hip": 96}
-SOURCES = ["attention_wave.hip", "attention_pair.hip", "attention.hip", "capi.hip", "qk_prepass.hip", "rot_q8.hip",
+AGPR_ALLOC = {"attention_pair.hip": 96, "attention_pp.hip": 96}
+SOURCES = ["attention_wave.hip", "attention_pair.hip", "attention_pp.hip", "attention.hip", "capi.hip", "qk_prepass.hip", "rot_q8.hip",
            "gemm.hip"]
 
 
@@ -54,7 +57,8 @@ def hipcc() -> str:
 
 def _run(cmd: list, what: str) -> None:
     r = subprocess.run(cmd, capture_output=True, text=True)
-    if r.returncode:
+    # hipcc's driver has returned 0 after a front-end error: its message counts as a failure too
+    if r.returncode or " error: " in r.stderr or "failed to execute" in r.stderr:
         raise RuntimeError(f"{what} failed:\n{' '.join(cmd)}\n{r.stdout}{r.stderr}")
 
 

@@ -42,6 +42,14 @@ constexpr int PAIR_BQ = 256;
 constexpr int PAIR_THREADS = 512;
 int launch_attention_pair(int vt, int ot, bool dump, const Exec &ex, const Arg *args, const AttnParams &p, int nqb,
                           const Split &sp, std::string *err);
+// The ping-pong kernel (attention_pp.hip): int8 scores, D = 128 without a causal mask, 8 waves (two per SIMD taking
+// turns between MFMA and softmax halves) over PP_BQ query rows. It reads V through a transposed copy in `vtbuf`
+// (attention_pp_vt_bytes(p) bytes of scratch), which the launch makes first.
+constexpr int PP_BQ = 256;
+constexpr int PP_THREADS = 512;
+size_t attention_pp_vt_bytes(const AttnParams &p);
+int launch_attention_pp(int vt, int ot, bool dump, const Exec &ex, const Arg *args, const AttnParams &p, int nqb,
+                        const Split &sp, char *vtbuf, std::string *err);
 
 
 namespace {

@@ -300,8 +300,8 @@ __device__ __attribute__((noinline)) void pair_body(const char *Q_, const char *
       const float p1 = __builtin_amdgcn_exp2f(fmaf(x[i + 1], qs_u, nm));
       const VP2 pp = {(VE)p0, (VE)p1};
       pr2[i >> 3][(i & 7) >> 1] = __builtin_bit_cast(int, pp);
-      if (i & 2) acc1 = sum2<VT>(pp, acc1);
-      else acc0 = sum2<VT>(pp, acc0);
+      if (i & 2) acc1 = (acc1 + p0) + p1;
+      else acc0 = (acc0 + p0) + p1;
     }
     return acc0 + acc1;
   };
@@ -370,13 +370,13 @@ __device__ __attribute__((noinline)) void pair_body(const char *Q_, const char *
 #pragma unroll
         for (int e = 0; e < 4; e++) xv[u][4 * g + e] = __builtin_amdgcn_exp2f(xv[u][4 * g + e]);
       };
-      auto PK = [&](int g, int u) {  // round to the value type into P, and sum the rounded values
+      auto PK = [&](int g, int u) {  // round to the value type into P; the row sums add the fp32 values (as nax.h:130 row_sum)
 #pragma unroll
         for (int e = 0; e < 4; e += 2) {
           const int i = 4 * g + e;
           const VP2 v2 = {(VE)xv[u][i], (VE)xv[u][i + 1]};
           pb[u][i >> 3][(i & 7) >> 1] = __builtin_bit_cast(int, v2);
-          la[u][e >> 1] = sum2<VT>(v2, la[u][e >> 1]);
+          la[u][e >> 1] = (la[u][e >> 1] + xv[u][i]) + xv[u][i + 1];
         }
       };
       // staging: K and scales of block j + 3, V of block j + 1
