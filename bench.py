@@ -205,8 +205,6 @@ def main():
     ap.add_argument("--config", default="c4", choices=sorted(CONFIGS))
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--cpu-budget", type=float, default=20.0)
-    ap.add_argument("--groups", type=int, default=0,
-                    help="attention kernel selector (the GROUPS macro: 0 default, 1 wave-pipelined, 3 paired, 4 ping-pong)")
     ap.add_argument("--extra", default="c2,c3,c5",
                     help="other configs timed in the same run and reported as extra keys ('' for none)")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
@@ -237,11 +235,10 @@ def main():
     kw, prepass, L = make_inputs(gpu, args.config, rng)
     O = gpu.empty((S, H * D), "bf16")
 
-    variant = {"GROUPS": args.groups} if args.groups else {}
 
     def step():
         ops.attention(gpu, kw["q"], kw["k"], kw["v"], O, Lq=S, L=L, H=H, KVH=H, D=D, q_rows=S, k_rows=S,
-                      scale=D ** -0.5, q_scale=kw.get("q_scale"), k_scale=kw.get("k_scale"), **variant)
+                      scale=D ** -0.5, q_scale=kw.get("q_scale"), k_scale=kw.get("k_scale"))
 
     for _ in range(args.warmup):
         step()
@@ -278,7 +275,7 @@ def main():
         "wall_ms_per_step": round(wall_s / args.steps * 1e3, 4),
         "roofline": {"bound": "mfma", "achieved": round(achieved / 1e12, 2), "peak": peak / 1e12,
                      "unit": "TFLOP/s", "frac": round(achieved / peak, 4), "traffic": traffic("attention_call"),
-                     "kernel": ("attention_pair_kernel" if args.groups == 3 else "attention_wave_kernel") + " (" +
+                     "kernel": "attention_wave_kernel (" +
                                ("int8 QK, bf16 PV" if path == "int8" else "bf16") + ") + attention_merge",
                      "per_launch_ms": round(per_launch * 1e3, 4)},
     }

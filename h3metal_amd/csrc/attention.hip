@@ -47,10 +47,7 @@
 //  * The 1-D grid is remapped so that each XCD (own L2) runs a contiguous
 //    range of (head, query-block) tiles, which then share one head's K/V in L2.
 //  * D = 128 without a causal mask (the DiT path) runs on the wave-pipelined
-//    kernel of attention_wave.hip by default. The macro GROUPS selects a kernel
-//    for A/B tests: 1 the wave-pipelined one, 2 this file's two-group kernel,
-//    3 the paired kernel of attention_pair.hip (two waves per SIMD; int8 scores
-//    only).
+//    kernel of attention_wave.hip; this file's kernel serves every other case.
 #include "attention_common.h"
 
 #include <algorithm>
@@ -560,40 +557,9 @@ int launch_attention(const Pipeline &pl, const Exec &ex, const Arg *args, int na
   const uint64_t qx = (uint64_t)(p.H - 1) * p.q_rows + p.Lq, kx = (uint64_t)(p.KVH - 1) * p.k_rows + p.L;
   if (!fits(0, qx * D * es, "q") || !fits(1, kx * D * es, "k") || !fits(2, kx * D * 2, "v")) return -1;
   if (qk8 && (!fits(5, qx * 4, "q_scale") || !fits(6, kx * 4, "k_scale"))) return -1;
-  // D = 128 without a causal mask: the paired kernel (int8 scores) or the wave-pipelined one (ival[2] = 2 / 1),
-  // unless GROUPS=2 selected this file's kernel (ival[2] = 0)
+  // D = 128 without a causal mask: the wave-pipelined kernel (ival[2] = 1)
   constexpr bool CANW = !CAUSAL && D == 128;
-  bool usew = CANW && pl.ival[2] != 0;
-  const bool usep = usew && QKT == T_I8 && pl.ival[2] == 2;
-  // the ping-pong kernel (ival[2] = 3, int8 scores) needs scratch for its transposed V besides the split's partial
-  // states; the context grows its scratch for it where it can (not in h3_dispatch_static: there an explicit GROUPS=4
-  // fails, the default falls back to the wave-pipelined kernel)
-  Exec exq = ex;
-  char *vtbuf = nullptr;
-  bool useq = usew && QKT == T_I8 && pl.ival[2] == 3;
-  if (useq) {
-    const size_t vtb = attention_pp_vt_bytes(p);
-    const size_t want = vtb + attention_workspace_max(cu_count());
-    if (exq.ws_bytes < want && exq.grow) {
-      void *nws = nullptr;
-      size_t nb = 0;
-      if (exq.grow(exq.owner, want, &nws, &nb) == 0) {
-        exq.ws = nws;
-        exq.ws_bytes = nb;
-      }
-    }
-    if (exq.ws_bytes >= vtb + 256) {
-      vtbuf = (char *)exq.ws;
-      exq.ws = (char *)exq.ws + vtb;
-      exq.ws_bytes -= vtb;
-    } else if (pl.ival[3]) {
-      *err = "the ping-pong kernel (GROUPS=4) needs " + std::to_string(vtb) + " bytes of scratch for V^T, the launch has " +
-             std::to_string(exq.ws_bytes);
-      return -1;
-    } else {
-      useq = false;  // the wave-pipelined kernel, which reads V as it is
-    }
-  }
+  const bool usew = CANW && pl.ival[2] != 0;
   // those kernels address a head's K/V rows (and the blocks their pipelines stage past the end) with 32-bit
   // byte offsets
   if (usew && (uint64_t)(p.L + 4 * BK) * D * 2 > 0xffffffffull) {
@@ -631,7 +597,7 @@ int launch_attention(const Pipeline &pl, const Exec &ex, const Arg *args, int na
     return -1;
   }
   if (p.Lq == 0) return 0;
-  const int BQ = useq ? PP_BQ : usep ? PAIR_BQ : usew ? WAVE_BQ : C::BQ;
+  const int BQ = usew ? WAVE_BQ : C::BQ;
   const int nqb = (p.Lq + BQ - 1) / BQ;
   const long ntiles = (long)nqb * p.H;
   if (ntiles > 0x7fffffffL / 256) {
@@ -648,22 +614,20 @@ int launch_attention(const Pipeline &pl, const Exec &ex, const Arg *args, int na
     const int R = (int)(ntiles % cus);
     // chunks per tile: at most CUs / R, at least 2 key blocks each, and as many as the scratch memory holds
     const size_t unit_bytes = (size_t)BQ * (D + 4) * sizeof(float);
-    const size_t fit = R ? exq.ws_bytes / (unit_bytes * R) : 0;
+    const size_t fit = R ? ex.ws_bytes / (unit_bytes * R) : 0;
     const int smax = R ? (int)std::min<size_t>(std::min(cus / R, kblocks / 2), fit) : 0;
     if (smax >= 2) {
       const int cb = (kblocks + smax - 1) / smax;
       sp.s = (kblocks + cb - 1) / cb;
       sp.cb = cb;
       sp.nfull = (int)ntiles - R;
-      sp.ws = (float *)exq.ws;
+      sp.ws = (float *)ex.ws;
     }
   }
   const long ngroups = sp.s ? (long)sp.nfull + (ntiles - sp.nfull) * sp.s : ntiles;
   // the scores hook of the older kernels writes the scores instead of the output
   char *out = DUMP && !usew ? args[7].ptr : args[3].ptr;
   if constexpr (CANW) {
-    if (useq) return launch_attention_pp(VT, OT, DUMP, exq, args, p, nqb, sp, vtbuf, err);
-    if (usep) return launch_attention_pair(VT, OT, DUMP, ex, args, p, nqb, sp, err);
     if (usew) return launch_attention_wave(QKT, VT, OT, DUMP, ex, args, p, nqb, sp, err);
   }
   auto kern = attention_kernel<D, QKT, VT, OT, CAUSAL, DUMP>;
@@ -726,13 +690,8 @@ int type_of(const std::string &s) {
 // as integers and do not change the gfx950 kernel (its tiles are its own).
 // SPLIT (this build's, default 1): allow the tail split of a partly filled
 // last round of workgroups; SPLIT=0 runs every tile whole. GROUPS (this
-// build's, default 0 = 1): HD 128 without a causal mask runs on the
-// wave-pipelined kernel; GROUPS=2 selects the two-group (ping-pong) kernel,
-// which also serves every other case, and GROUPS=3 the paired kernel (int8).
-// Whether GROUPS=0 runs int8 scores on the ping-pong kernel (else on the wave-pipelined kernel).
-#ifndef PP_DEFAULT
-#define PP_DEFAULT 0
-#endif
+// build's) 0 or 1: the wave-pipelined kernel for HD 128 without a causal mask
+// (the values that selected other kernels for it are refused).
 bool make_attention(const std::string &fn, const Macros &m, Pipeline *pl, std::string *err) {
   const bool dump = fn == "attention_scores";
   if (fn != "attention" && !dump) {
@@ -747,12 +706,9 @@ bool make_attention(const std::string &fn, const Macros &m, Pipeline *pl, std::s
     if (!macro_int(m, k, 0, &dummy, err)) return false;
   int split, groups;
   if (!macro_int(m, "SPLIT", 1, &split, err) || !macro_int(m, "GROUPS", 0, &groups, err)) return false;
-  if (groups < 0 || groups > 4) {
-    *err = "GROUPS must be 0 (default), 1, 2, 3 or 4";
-    return false;
-  }
-  if ((groups == 3 || groups == 4) && !qk8) {
-    *err = "GROUPS=3 (the paired kernel) and GROUPS=4 (the ping-pong kernel) need int8 scores (QK8=1)";
+  if (groups < 0 || groups > 1) {
+    *err = "GROUPS must be 0 or 1 (the wave-pipelined kernel; the paired, ping-pong and two-group kernels that 2-4 "
+           "selected for HD 128 without a causal mask are retired)";
     return false;
   }
   for (auto &kv : m) {
@@ -781,15 +737,12 @@ bool make_attention(const std::string &fn, const Macros &m, Pipeline *pl, std::s
   else if (hd == 96) f = dump ? pick_types<96, true>(qkt, it, ot, causal) : pick_types<96, false>(qkt, it, ot, causal);
   else f = dump ? pick_types<64, true>(qkt, it, ot, causal) : pick_types<64, false>(qkt, it, ot, causal);
   pl->launch = f;
-  // the kernel the pipeline launches for HD 128 without a causal mask: 1 the wave-pipelined kernel (the default
-  // for 16-bit scores), 2 the paired kernel (int8 scores), 3 the ping-pong kernel (int8 scores), 0 this file's
-  // two-group kernel (which serves every other case)
-  int ksel = 0;
-  if (hd == 128 && !causal) ksel = groups == 1 ? 1 : groups == 3 ? 2 : groups == 4 ? 3 : groups == 2 ? 0 : PP_DEFAULT && qk8 ? 3 : 1;
-  pl->threads = ksel == 3 ? PP_THREADS : ksel == 2 ? PAIR_THREADS : ksel == 1 ? WAVE_THREADS : NW * 64;
+  // the kernel the pipeline launches: 1 the wave-pipelined kernel (HD 128 without a causal mask), 0 this file's
+  // two-group kernel (every other case)
+  const int ksel = hd == 128 && !causal ? 1 : 0;
+  pl->threads = ksel == 1 ? WAVE_THREADS : NW * 64;
   pl->ival[0] = split != 0;
   pl->ival[2] = ksel;
-  pl->ival[3] = groups == 4;  // the ping-pong kernel chosen explicitly (no fallback)
   return true;
 }
 

@@ -36,21 +36,6 @@ constexpr int WAVE_BQ = 128 * WAVE_NU;  // query rows per workgroup of the wave-
 constexpr int WAVE_THREADS = 256;       // its workgroup: 4 waves, one per SIMD
 int launch_attention_wave(int qkt, int vt, int ot, bool dump, const Exec &ex, const Arg *args, const AttnParams &p,
                           int nqb, const Split &sp, std::string *err);
-// The paired kernel (attention_pair.hip): int8 scores, D = 128 without a causal mask, 8 waves (two per SIMD) over
-// PAIR_BQ query rows; vt, ot as above.
-constexpr int PAIR_BQ = 256;
-constexpr int PAIR_THREADS = 512;
-int launch_attention_pair(int vt, int ot, bool dump, const Exec &ex, const Arg *args, const AttnParams &p, int nqb,
-                          const Split &sp, std::string *err);
-// The ping-pong kernel (attention_pp.hip): int8 scores, D = 128 without a causal mask, 8 waves (two per SIMD taking
-// turns between MFMA and softmax halves) over PP_BQ query rows. It reads V through a transposed copy in `vtbuf`
-// (attention_pp_vt_bytes(p) bytes of scratch), which the launch makes first.
-constexpr int PP_BQ = 256;
-constexpr int PP_THREADS = 512;
-size_t attention_pp_vt_bytes(const AttnParams &p);
-int launch_attention_pp(int vt, int ot, bool dump, const Exec &ex, const Arg *args, const AttnParams &p, int nqb,
-                        const Split &sp, char *vtbuf, std::string *err);
-
 
 namespace {
 

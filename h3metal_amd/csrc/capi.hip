@@ -432,16 +432,6 @@ static int dispatch(h3_ctx *ctx, void *pso, const h3_arg *bufs, int nbufs, const
   ex.stream = ctx->stream;
   ex.ws = no_alloc ? ctx->static_ws : ctx->ws;
   ex.ws_bytes = no_alloc ? h3::STATIC_SCRATCH_BYTES_VALUE : ctx->ws_bytes;
-  if (!no_alloc) {
-    ex.owner = ctx;
-    ex.grow = [](void *owner, size_t bytes, void **ws, size_t *ws_bytes) -> int {
-      auto *c = static_cast<h3_ctx *>(owner);
-      if (h3_reserve_workspace(c, bytes)) return -1;
-      *ws = c->ws;
-      *ws_bytes = c->ws_bytes;
-      return 0;
-    };
-  }
   int rc = pl->launch(*pl, ex, args, nbufs, params, params_len, &err);
   if (rc) {
     set_error(pl->name + ": " + err);

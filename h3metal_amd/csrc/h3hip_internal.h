@@ -73,10 +73,6 @@ struct Exec {
   hipStream_t stream = nullptr;
   void *ws = nullptr;
   size_t ws_bytes = 0;
-  // Grows the scratch memory to at least `bytes` (waiting for the stream's queued work first) and returns 0 with
-  // the new buffer in *ws / *ws_bytes, or -1; null where the caller cannot allocate (h3_dispatch_static).
-  int (*grow)(void *owner, size_t bytes, void **ws, size_t *ws_bytes) = nullptr;
-  void *owner = nullptr;
 };
 
 // Size of the fixed scratch array that h3_dispatch_static uses instead of the context's workspace.

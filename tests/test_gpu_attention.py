@@ -58,13 +58,11 @@ def run_attention(gpu, q, k, v, *, dtype, Lq, L, H, KVH, D, scale, causal=False,
 
 # -- int32 / fp32 score accumulators -------------------------------------------------------------------------------
 
-@pytest.mark.parametrize("groups", [1, 3, 4, 2])
 @pytest.mark.parametrize("Lq,L,H,KVH,D", [(100, 100, 2, 2, 128), (77, 300, 3, 3, 128), (64, 64, 4, 1, 64),
                                           (300, 1037, 2, 1, 128), (1, 5, 1, 1, 128), (700, 449, 2, 2, 128)])
-def test_int32_scores_bit_exact(gpu, Lq, L, H, KVH, D, groups):
-    """int32 score accumulators of the kernel that runs equal the exact integer products (int8, D=128: GROUPS=1 the
-    wave-pipelined kernel (the default), 3 the paired kernel, 4 the ping-pong kernel, 2 the two-group kernel; D=64
-    always the two-group one)."""
+def test_int32_scores_bit_exact(gpu, Lq, L, H, KVH, D):
+    """int32 score accumulators of the kernel that runs equal the exact integer products (int8: D=128 the
+    wave-pipelined kernel, D=64 the two-group one)."""
     rng = np.random.default_rng(Lq + L)
     qi = rng.integers(-127, 128, (H, Lq, D)).astype(np.int8)
     ki = rng.integers(-127, 128, (KVH, L, D)).astype(np.int8)
@@ -75,9 +73,9 @@ def test_int32_scores_bit_exact(gpu, Lq, L, H, KVH, D, groups):
     V = gpu.empty((KVH, k_rows, D), "bf16")
     qs, ks = gpu.upload(np.ones((H, q_rows), np.float32)), gpu.upload(np.ones((KVH, k_rows), np.float32))
     S = gpu.empty((H, Lq, L), "i32")
-    print(f"[scores] groups={groups} Lq={Lq} L={L} H={H} KVH={KVH} D={D}", flush=True)
+    print(f"[scores] Lq={Lq} L={L} H={H} KVH={KVH} D={D}", flush=True)
     ops.attention_scores(gpu, Q, K, V, S, Lq=Lq, L=L, H=H, KVH=KVH, D=D, q_rows=q_rows, k_rows=k_rows,
-                         q_scale=qs, k_scale=ks, GROUPS=groups)
+                         q_scale=qs, k_scale=ks)
     gpu.wait()
     want = oa.int_scores(qi, ki, H_per_kv=H // KVH)
     got = S.numpy()
@@ -565,10 +563,9 @@ def test_tail_split_matches_whole_tiles(gpu, q8_path):
 
 
 @pytest.mark.parametrize("H,KVH,Lq,L,seq", [(4, 4, 1000, 1500, None), (6, 2, 777, 2049, None), (4, 4, 300, 700, 2)])
-def test_int8_paired_kernel_matches_other_kernels(gpu, H, KVH, Lq, L, seq):
-    """int8 scores at D=128 without a causal mask run on the wave-pipelined kernel by default (GROUPS=0 / 1);
-    GROUPS=3 / 4 / 2 select the paired (two waves per SIMD), the ping-pong (two waves per SIMD taking turns, V
-    transposed first) and the two-group kernels. Same inputs through all,
+def test_int8_split_and_whole_tiles_agree(gpu, H, KVH, Lq, L, seq):
+    """int8 scores at D=128 without a causal mask (the wave-pipelined kernel), the default GROUPS=0 and the
+    explicit GROUPS=1, with the tail split and without (SPLIT=0). Same inputs through all,
     with and without the tail split: every output meets the tolerance against float64 and the kernels agree to
     rounding. Ragged L (a partly masked last key block), GQA, several 256-row query blocks per head and batched
     sequences (seq_heads) included."""
@@ -583,7 +580,7 @@ def test_int8_paired_kernel_matches_other_kernels(gpu, H, KVH, Lq, L, seq):
     seq_heads = seq or H
     nseq = H // seq_heads
     outs = []
-    for groups, split in ((0, 1), (3, 0), (4, 1), (4, 0), (1, 1), (1, 0), (2, 1)):
+    for groups, split in ((0, 1), (1, 1), (1, 0)):
         print(f"[attention] groups={groups} split={split} H={H} KVH={KVH} Lq={Lq} L={L} seq={seq}", flush=True)
         O = gpu.empty((nseq * qr, seq_heads * D), "f32")
         ops.attention(gpu, Q, K, V, O, Lq=Lq, L=L, H=H, KVH=KVH, D=D, q_rows=qr, k_rows=kr, scale=D ** -0.5,
@@ -602,23 +599,19 @@ def test_int8_paired_kernel_matches_other_kernels(gpu, H, KVH, Lq, L, seq):
 
 
 def test_groups_macro_refused(gpu):
-    """GROUPS accepts 0 to 4 only, and 3 (the paired kernel) and 4 (the ping-pong kernel) only with int8 scores
-    (checked on the host when the pipeline is made)."""
+    """GROUPS accepts 0 and 1 only (the values 2-4 selected kernels that are retired; checked on the host when the
+    pipeline is made)."""
     from h3metal_amd.gpu import GpuError
-    with pytest.raises(GpuError, match="GROUPS"):
-        gpu.kernel("attention", "attention", HD=128, QK8=1, IN_T="bfloat", O_T="bfloat", GROUPS=5)
-    with pytest.raises(GpuError, match="GROUPS=3"):
-        gpu.kernel("attention", "attention", HD=128, QK8=0, IN_T="bfloat", O_T="bfloat", GROUPS=3)
-    with pytest.raises(GpuError, match="GROUPS=4"):
-        gpu.kernel("attention", "attention", HD=128, QK8=0, IN_T="bfloat", O_T="bfloat", GROUPS=4)
+    for g in (2, 3, 4, 5):
+        with pytest.raises(GpuError, match="GROUPS must be 0 or 1"):
+            gpu.kernel("attention", "attention", HD=128, QK8=1, IN_T="bfloat", O_T="bfloat", GROUPS=g)
 
 
 @pytest.mark.parametrize("Lq,L", [(1, 1), (5, 63), (384, 64), (385, 65), (17, 129), (700, 191), (64, 31), (65, 33),
                                   (257, 97), (200, 160)])
-@pytest.mark.parametrize("groups", [1, 3, 4])
-def test_int8_kernel_edges(gpu, Lq, L, groups):
-    """Edge shapes through the wave-pipelined (GROUPS=1), paired (GROUPS=3) and ping-pong kernels (GROUPS=4; int8,
-    D=128, no causal mask): one query or one key, key counts around the 64-key block and the 32-key halves of the paired kernel
+def test_int8_kernel_edges(gpu, Lq, L):
+    """Edge shapes through the wave-pipelined kernel (int8, D=128, no causal mask): one query or one key, key counts
+    around the 64-key block and its 32-key tiles
     (the last block's rows past L load as zeros and are masked), query counts around the 64-row pairs and the
     256-row tiles. Checked against float64 within the north-star tolerance."""
     rng = np.random.default_rng(Lq * 1000 + L)
@@ -629,9 +622,9 @@ def test_int8_kernel_edges(gpu, Lq, L, groups):
     v = to_bf16(rng.standard_normal((H, L, D)).astype(np.float32))
     Q, K, V = padded(gpu, qi, qr, "i8"), padded(gpu, ki, kr, "i8"), padded(gpu, v, kr, "bf16")
     O = gpu.empty((qr, H * D), "f32")
-    print(f"[attention] edge groups={groups} Lq={Lq} L={L}", flush=True)
+    print(f"[attention] edge Lq={Lq} L={L}", flush=True)
     ops.attention(gpu, Q, K, V, O, Lq=Lq, L=L, H=H, KVH=H, D=D, q_rows=qr, k_rows=kr, scale=D ** -0.5,
-                  q_scale=padded(gpu, qs, qr, "f32"), k_scale=padded(gpu, ks, kr, "f32"), GROUPS=groups)
+                  q_scale=padded(gpu, qs, qr, "f32"), k_scale=padded(gpu, ks, kr, "f32"))
     gpu.wait()
     got = O.numpy().astype(np.float64)
     ref = oa.ref_attention(qi * qs[..., None].astype(np.float64), ki * ks[..., None].astype(np.float64),
@@ -656,13 +649,12 @@ def test_key_count_beyond_32bit_offsets_refused(gpu):
                       q_scale=qs, k_scale=ks)
 
 
-@pytest.mark.parametrize("path", ["int8", "int8-pp", "bf16", "f16"])
+@pytest.mark.parametrize("path", ["int8", "bf16", "f16"])
 def test_scores_rising_far_above_the_first_block(gpu, path):
     """Key scores that rise by ~100 log2 units from the first keys to the last (a ramp on one channel shared by
     every query), so that each row's reference maximum is passed by more than the accepted growth several times
     (2^30 per block with bf16 P, 2^15 with f16 P): the recomputed blocks and the rescaled O and l against float64
-    attention, at the north-star tolerance. int8-pp: the ping-pong kernel (GROUPS=4), whose check is on the packed
-    P bits."""
+    attention, at the north-star tolerance."""
     rng = np.random.default_rng(77)
     H, Lq, L, D = 2, 130, 1100, 128
     q = rng.standard_normal((H, Lq, D)).astype(np.float32)
@@ -670,13 +662,12 @@ def test_scores_rising_far_above_the_first_block(gpu, path):
     v = rng.standard_normal((H, L, D)).astype(np.float32)
     q[..., 0] = 8.0
     k[..., 0] = np.linspace(-50.0, 50.0, L, dtype=np.float32)
-    if path.startswith("int8"):
+    if path == "int8":
         qi, qs = q8(q)
         ki, ks = q8(k)
         vb = to_bf16(v)
-        variant = dict(GROUPS=4) if path == "int8-pp" else {}
         got = run_attention(gpu, qi, ki, vb, dtype="bf16", Lq=Lq, L=L, H=H, KVH=H, D=D, scale=D ** -0.5, qs=qs,
-                            ks=ks, out_dt="f32", **variant)
+                            ks=ks, out_dt="f32")
         ref = oa.ref_attention(qi * qs[..., None].astype(np.float64), ki * ks[..., None].astype(np.float64),
                                from_bf16(vb), D ** -0.5)
     elif path == "bf16":

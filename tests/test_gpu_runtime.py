@@ -44,9 +44,6 @@ def test_unknown_kernel_and_macros(gpu):
     assert k.max_threads == 256  # the wave-pipelined kernel's workgroup
     assert gpu.kernel("attention", "attention", HD=128, O_T="bfloat").max_threads == 256
     assert gpu.kernel("attention", "attention", HD=128, QK8=1, O_T="bfloat", GROUPS=1).max_threads == 256
-    assert gpu.kernel("attention", "attention", HD=128, QK8=1, O_T="bfloat", GROUPS=3).max_threads == 512
-    assert gpu.kernel("attention", "attention", HD=128, QK8=1, O_T="bfloat", GROUPS=4).max_threads == 512
-    assert gpu.kernel("attention", "attention", HD=128, QK8=1, O_T="bfloat", GROUPS=2).max_threads == 512
     assert gpu.kernel("attention", "attention", HD=128, QK8=1, O_T="bfloat", CAUSAL=1).max_threads == 512
 
 
