@@ -113,6 +113,14 @@ void attention_wave_kernel(const char *__restrict__ Q, const char *__restrict__ 
   extern __shared__ __attribute__((aligned(16))) char smem[];
   const unsigned lds0 = (unsigned)(size_t)(__attribute__((address_space(3))) char *)smem;
 
+#ifdef WAVE_TIMING2
+  // timing-only builds: shader-clock ticks at entry, at the first key step and after the last P V, and the real
+  // time (100 MHz) at entry and after the last P V, written to the output's first bytes (no output is written)
+  __builtin_amdgcn_sched_barrier(0);
+  const unsigned long long t_entry = __builtin_amdgcn_s_memtime(), r_entry = __builtin_amdgcn_s_memrealtime();
+  __builtin_amdgcn_sched_barrier(0);
+  unsigned long long t_loop = 0;
+#endif
   const int tid = threadIdx.x, lane = tid & 63, hl = lane >> 5, l32 = lane & 31;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int b = blockIdx.x;
@@ -199,7 +207,7 @@ void attention_wave_kernel(const char *__restrict__ Q, const char *__restrict__ 
     vgo[r] = row * (D * 2) + (2 * (uu ^ (2 * (row & 3))) + sub) * 16;
   }
   auto stage_k = [&](int blk) {  // K and key scales of block blk
-    const int slot = blk % NRV;
+    const int slot = blk & (NRV - 1);
     const unsigned kb0 = (unsigned)kblk(blk) * (BK * C::RB);
 #pragma unroll
     for (int r = 0; r < C::KDMA; r++) dma16(lds0 + C::KOFF + slot * C::KBYTES + (r * NWV + w) * 1024, kgo[r] + kb0, rk);
@@ -211,13 +219,13 @@ void attention_wave_kernel(const char *__restrict__ Q, const char *__restrict__ 
   constexpr int NLOADS = C::KDMA + (QK8 ? 1 : 0) + C::VDMA;
   auto stage_one = [&](int i, int kb, int vb) {
     if (i < C::KDMA) {
-      dma16(lds0 + C::KOFF + (kb % NRV) * C::KBYTES + (i * NWV + w) * 1024,
+      dma16(lds0 + C::KOFF + (kb & (NRV - 1)) * C::KBYTES + (i * NWV + w) * 1024,
             kgo[i] + (unsigned)kblk(kb) * (BK * C::RB), rk);
     } else if (QK8 && i == C::KDMA) {
-      dma4(lds0 + C::SOFF + (kb % NRV) * BK * 4, lane * 4 + (unsigned)kblk(kb) * (BK * 4), rs);
+      dma4(lds0 + C::SOFF + (kb & (NRV - 1)) * BK * 4, lane * 4 + (unsigned)kblk(kb) * (BK * 4), rs);
     } else {
       const int r = i - C::KDMA - (QK8 ? 1 : 0);
-      dma16(lds0 + C::VOFF + (vb % NRV) * C::VBYTES + (r * NWV + w) * 1024,
+      dma16(lds0 + C::VOFF + (vb & (NRV - 1)) * C::VBYTES + (r * NWV + w) * 1024,
             vgo[r] + (unsigned)kblk(vb) * (BK * D * 2), rv);
     }
   };
@@ -225,7 +233,7 @@ void attention_wave_kernel(const char *__restrict__ Q, const char *__restrict__ 
     const unsigned vb0 = (unsigned)kblk(blk) * (BK * D * 2);
 #pragma unroll
     for (int r = 0; r < C::VDMA; r++)
-      dma16(lds0 + C::VOFF + (blk % NRV) * C::VBYTES + (r * NWV + w) * 1024, vgo[r] + vb0, rv);
+      dma16(lds0 + C::VOFF + (blk & (NRV - 1)) * C::VBYTES + (r * NWV + w) * 1024, vgo[r] + vb0, rv);
   };
 
   f32x16 o[NU][D / 32];
@@ -273,7 +281,7 @@ void attention_wave_kernel(const char *__restrict__ Q, const char *__restrict__ 
 
   // K operands of key tile t of block j (A of S^T = K Q^T)
   auto kops = [&](int j, int t, i32x4 (&ka)[C::NCH]) {
-    const char *Ks = smem + C::KOFF + (j % NRV) * C::KBYTES + 32 * t * C::RB;
+    const char *Ks = smem + C::KOFF + (j & (NRV - 1)) * C::KBYTES + 32 * t * C::RB;
 #pragma unroll
     for (int c = 0; c < C::NCH; c++) ka[c] = *(const i32x4 *)(Ks + kbase[c]);
   };
@@ -294,7 +302,7 @@ void attention_wave_kernel(const char *__restrict__ Q, const char *__restrict__ 
   };
   // V operands of key tile t of block j: [16-key step][channel block]
   auto vops = [&](int j, int t, i16x8 (&va)[2][D / 32]) {
-    const char *Vs = smem + C::VOFF + (j % NRV) * C::VBYTES;
+    const char *Vs = smem + C::VOFF + (j & (NRV - 1)) * C::VBYTES;
 #pragma unroll
     for (int s2 = 0; s2 < 2; s2++) {
       const int koff = (32 * t + 16 * s2) * (D * 2);
@@ -308,7 +316,7 @@ void attention_wave_kernel(const char *__restrict__ Q, const char *__restrict__ 
   };
   // key scales of key tile t of block j, for this lane's 16 keys
   auto kscales = [&](int j, int t, f32x4 (&k4)[2][2]) {
-    const float *ksc = (const float *)(smem + C::SOFF) + (j % NRV) * BK;
+    const float *ksc = (const float *)(smem + C::SOFF) + (j & (NRV - 1)) * BK;
 #pragma unroll
     for (int s8 = 0; s8 < 2; s8++)
 #pragma unroll
@@ -384,16 +392,16 @@ void attention_wave_kernel(const char *__restrict__ Q, const char *__restrict__ 
     f32x4 c4[4];  // -SEED_F * k4 (int8), made in the query tile 0 sub-tile for both query tiles
   };
   auto vread = [&](int j, int t, int k) {  // V(j) operand k of key tile t
-    const char *Vs = smem + C::VOFF + (j % NRV) * C::VBYTES + (32 * t + 16 * (k >> 2)) * (D * 2) + vbase[k & 3];
+    const char *Vs = smem + C::VOFF + (j & (NRV - 1)) * C::VBYTES + (32 * t + 16 * (k >> 2)) * (D * 2) + vbase[k & 3];
     const i16x4 lo = lds_tr16(Vs);
     const i16x4 hi = lds_tr16(Vs + 4 * (D * 2));
     return i16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
   };
   auto kread = [&](int j, int t, int c) {  // K(j) operand, chunk c of key tile t
-    return *(const i32x4 *)(smem + C::KOFF + (j % NRV) * C::KBYTES + 32 * t * C::RB + kbase[c]);
+    return *(const i32x4 *)(smem + C::KOFF + (j & (NRV - 1)) * C::KBYTES + 32 * t * C::RB + kbase[c]);
   };
   auto sread = [&](int j, int t, int g) {  // scales of K(j), score group g of key tile t
-    return *(const f32x4 *)((const float *)(smem + C::SOFF) + (j % NRV) * BK + 32 * t + 16 * (g >> 1) + 8 * hl +
+    return *(const f32x4 *)((const float *)(smem + C::SOFF) + (j & (NRV - 1)) * BK + 32 * t + 16 * (g >> 1) + 8 * hl +
                             4 * (g & 1));
   };
   auto load_ops = [&](Ops &op, int j, int t) {  // all operands of tile t of step j
@@ -418,7 +426,7 @@ void attention_wave_kernel(const char *__restrict__ Q, const char *__restrict__ 
       if (u == 0) {  // the seed corrections of this key tile, shared by both query tiles
 #pragma unroll
         for (int g = 0; g < 4; g++)
-          op.c4[g] = *(const f32x4 *)((const float *)(smem + C::COFF) + (j % NRV) * BK + 32 * t + 16 * (g >> 1) +
+          op.c4[g] = *(const f32x4 *)((const float *)(smem + C::COFF) + (j & (NRV - 1)) * BK + 32 * t + 16 * (g >> 1) +
                                       8 * hl + 4 * (g & 1));
       }
     }
@@ -556,9 +564,9 @@ void attention_wave_kernel(const char *__restrict__ Q, const char *__restrict__ 
     // the scales of block j + 2 landed before this barrier: their seed corrections, published by the next one
     // (every wave writes the same 64 values)
     float kv = 0.0f;
-    if constexpr (QK8 && SEEDED) kv = ((const float *)(smem + C::SOFF))[((j + 2) % NRV) * BK + lane];
+    if constexpr (QK8 && SEEDED) kv = ((const float *)(smem + C::SOFF))[((j + 2) & (NRV - 1)) * BK + lane];
     sub_tile(op, j, 1, NU - 1, has_pv, has_next, mask, true, j + 1, 0, la[NU - 1], 0, KS + (C::VDMA - VE0), j);
-    if constexpr (QK8 && SEEDED) ((float *)(smem + C::COFF))[((j + 2) % NRV) * BK + lane] = kv * -SEED_F;
+    if constexpr (QK8 && SEEDED) ((float *)(smem + C::COFF))[((j + 2) & (NRV - 1)) * BK + lane] = kv * -SEED_F;
     tick(4);
     tot[NU - 1] = (la[NU - 1][0] + la[NU - 1][1]) + (la[NU - 1][2] + la[NU - 1][3]);
     bad = bad | !(tot[NU - 1] - l[NU - 1] <= sum_limit<VT>());
@@ -632,10 +640,16 @@ void attention_wave_kernel(const char *__restrict__ Q, const char *__restrict__ 
     }
     Ops op;
     load_ops(op, 0, 0);
+#ifdef WAVE_TIMING2
+    __builtin_amdgcn_sched_barrier(0);
+    t_loop = __builtin_amdgcn_s_memtime();
+    __builtin_amdgcn_sched_barrier(0);
+#endif
     // first block (no P V yet), the steady state (no masking: every key of the block is valid), the last block
     if (nblk == 1) step(op, 0, false, false, true);
     else step(op, 0, false, true, false);
-    for (int j = 1; j + 1 < nblk; j++) step(op, j, true, true, false);
+    int j = 1;
+    for (; j + 1 < nblk; j++) step(op, j, true, true, false);
     if (nblk > 1) step(op, nblk - 1, true, false, true);
     // P V of the last block (its tile-0 V operands were read by the last step)
 #pragma unroll
@@ -653,6 +667,23 @@ void attention_wave_kernel(const char *__restrict__ Q, const char *__restrict__ 
     o_fence(o);  // inside the branch: no copy of O may come between the last MFMA and the fence
   }
 
+#ifdef WAVE_TIMING2
+  {
+    __builtin_amdgcn_sched_barrier(0);
+    const unsigned long long t_end = __builtin_amdgcn_s_memtime(), r_end = __builtin_amdgcn_s_memrealtime();
+    if (lane == 0) {
+      long long *tp = (long long *)O + ((size_t)blockIdx.x * NWV + w) * 8;
+      tp[0] = (long long)t_entry;
+      tp[1] = (long long)t_loop;
+      tp[2] = (long long)t_end;
+      tp[3] = (long long)r_entry;
+      tp[4] = (long long)r_end;
+      tp[5] = blockIdx.x;
+      tp[7] = nblk;
+    }
+    return;
+  }
+#endif
 #ifdef WAVE_TIMING
   // the output's first bytes carry the ticks (workgroup b, wave w at 64 (NWV b + w)); no output is written
   if (lane == 0) {
