@@ -146,7 +146,8 @@ class QWeight:
 
 def gemm(gpu: Gpu, a: Tensor, wt: QWeight, out: Tensor, M: int, *, sa: Tensor | None = None, epi: int = 0,
          rtype: Tensor | None = None, gate: Tensor | None = None, g_stride: int = 0, c_stride: int | None = None,
-         a_stride: int | None = None, tile=(64, 128, 4), swz: int = 1, ksplit: int = 1, _low=None):
+         a_stride: int | None = None, tile=(64, 128, 4), swz: int = 1, ksplit: int = 1, no_alloc: bool = False,
+         _low=None):
     """out = A x W^T (epi 0), or out += gate[rtype] * (A x W^T) (epi 1, out float), plus bias[n]:
       q8:  A int8 [M][K] with row scales sa, W int8 codes, v = sa[m] * sw[n] * (a_m . w_n)
       h8:  A half, W int8 codes, v = sw[n] * (a_m . w_n)
@@ -154,7 +155,9 @@ def gemm(gpu: Gpu, a: Tensor, wt: QWeight, out: Tensor, M: int, *, sa: Tensor | 
 
     ksplit: accumulate over that many consecutive slices of K in separate dispatches (epi 1 only), as the
     reference does. tile / swz are the Metal kernel's tile choices: checked as the reference checks them (the
-    tile width must divide N) and otherwise unused (the gfx950 kernel uses 256 x 256 tiles and covers any N)."""
+    tile width must divide N) and otherwise unused (the gfx950 kernel uses 256 x 256 tiles and covers any N).
+    no_alloc: dispatch through the allocation-free entry point (h3_dispatch_static); the h8 format's widened
+    weights then live in its fixed scratch array."""
     if wt.fmt not in GEMM_ACT:
         raise NotImplementedError(f"gemm: weight format {wt.fmt!r} is not built (q8, h8, f16, bf16)")
     if a.dtype != GEMM_ACT[wt.fmt]:
@@ -169,7 +172,8 @@ def gemm(gpu: Gpu, a: Tensor, wt: QWeight, out: Tensor, M: int, *, sa: Tensor | 
             part = replace(wt, w=wt.w.view((wt.N, kp), offset_elems=i * kp), K=kp, ws=wt.w_stride,
                            bias=wt.bias if i == 0 else None)
             gemm(gpu, a.view((a.shape[0], kp), offset_elems=i * kp), part, out, M, sa=sa, epi=1, rtype=rtype,
-                 gate=gate, g_stride=g_stride, c_stride=c_stride, a_stride=a_stride or wt.K, tile=tile, swz=swz)
+                 gate=gate, g_stride=g_stride, c_stride=c_stride, a_stride=a_stride or wt.K, tile=tile, swz=swz,
+                 no_alloc=no_alloc)
         return
     tm, tn, nsg = tile
     if wt.N % tn:
@@ -184,4 +188,5 @@ def gemm(gpu: Gpu, a: Tensor, wt: QWeight, out: Tensor, M: int, *, sa: Tensor | 
     m_pad = (M + tm - 1) // tm * tm
     params = pack("8i", m_pad, wt.N, wt.K, a_stride or wt.K, c_stride or wt.N, wt.w_stride, wt.K // wt.G,
                   g_stride or wt.N)
-    gpu.launch(k, None, None, [a, wt.w, wt.sw, sa, out, wt.bias, rtype, gate], params, params_index=8)
+    gpu.launch(k, None, None, [a, wt.w, wt.sw, sa, out, wt.bias, rtype, gate], params, params_index=8,
+               no_alloc=no_alloc)

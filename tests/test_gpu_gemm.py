@@ -24,7 +24,7 @@ def make(rng, M, N, K, m_pad=None, bias=False):
     return a, sa, q, sw, b
 
 
-def run(gpu, a, sa, q, sw, b, M, out_dtype="f32", tile=(64, 128, 4)):
+def run(gpu, a, sa, q, sw, b, M, out_dtype="f32", tile=(64, 128, 4), no_alloc=False):
     N, K = q.shape
     print(f"[gemm] M={M} N={N} K={K} out={out_dtype} bias={b is not None}", flush=True)
     wt = ops.QWeight("q8", gpu.upload(q), gpu.upload(sw), N, K, bias=gpu.upload(b) if b is not None else None)
@@ -32,7 +32,7 @@ def run(gpu, a, sa, q, sw, b, M, out_dtype="f32", tile=(64, 128, 4)):
     A = gpu.upload(np.pad(a, ((0, max(0, m_pad - a.shape[0])), (0, 0))))
     SA = gpu.upload(np.pad(sa, (0, max(0, m_pad - sa.shape[0]))))
     out = gpu.empty((m_pad, N), out_dtype)
-    ops.gemm(gpu, A, wt, out, M, sa=SA, tile=tile)
+    ops.gemm(gpu, A, wt, out, M, sa=SA, tile=tile, no_alloc=no_alloc)
     gpu.wait()
     return out.numpy()[:M]
 
@@ -176,10 +176,12 @@ def test_config4_projection_shapes_sampled(gpu):
 
 
 @pytest.mark.parametrize("mode", ["f32", "bf16", "epi1"])
-def test_last_round_rows_on_small_tiles(gpu, mode):
+@pytest.mark.parametrize("no_alloc", [False, True])
+def test_last_round_rows_on_small_tiles(gpu, mode, no_alloc):
     """260 tiles of 256 x 256 on 256 CUs: the last row of tiles (rows 16384..16447) runs as a second launch of
     128 x 128 tiles on the sub-problem of those rows; every row bit for bit (f32, the residual form) or equal to
-    the rounded oracle (bf16), the rows of both launches alike."""
+    the rounded oracle (bf16), the rows of both launches alike; through h3_dispatch and through the
+    allocation-free entry point h3_dispatch_static."""
     rng = np.random.default_rng(46)
     M, N, K = 16448, 1024, 128
     a, sa, q, sw, b = make(rng, M, N, K, bias=True)
@@ -190,14 +192,14 @@ def test_last_round_rows_on_small_tiles(gpu, mode):
         gates = rng.standard_normal((3, N)).astype(np.float32)
         wt = ops.QWeight("q8", gpu.upload(q), gpu.upload(sw), N, K, bias=gpu.upload(b))
         X = gpu.upload(x0)
-        print(f"[gemm] tail rows M={M} N={N} K={K} epi=1", flush=True)
+        print(f"[gemm] tail rows M={M} N={N} K={K} epi=1 no_alloc={no_alloc}", flush=True)
         ops.gemm(gpu, gpu.upload(a), wt, X, M, sa=gpu.upload(sa), epi=1, rtype=gpu.upload(types),
-                 gate=gpu.upload(gates), tile=(64, 256, 8))
+                 gate=gpu.upload(gates), tile=(64, 256, 8), no_alloc=no_alloc)
         gpu.wait()
         want = og.residual(x0, v, gates, types)
         assert np.array_equal(X.numpy().view(np.uint32), want.view(np.uint32))
         return
-    got = run(gpu, a, sa, q, sw, b, M, out_dtype=mode)
+    got = run(gpu, a, sa, q, sw, b, M, out_dtype=mode, no_alloc=no_alloc)
     if mode == "f32":
         assert np.array_equal(got.view(np.uint32), v.view(np.uint32))
     else:

@@ -49,7 +49,7 @@ class FakeGpu:
         self.kernels.append((file, fn, macros))
         return (file, fn, tuple(sorted(macros.items())))
 
-    def launch(self, k, grid, threads, args, params=b"", params_index=None, tg_mem=0):
+    def launch(self, k, grid, threads, args, params=b"", params_index=None, tg_mem=0, no_alloc=False):
         self.launches.append((k, args, params, params_index))
 
 
