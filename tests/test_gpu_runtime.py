@@ -125,6 +125,22 @@ def test_device_copy(gpu):
         A.copy_to(B.view((4000,), offset_elems=8000))
 
 
+@pytest.mark.parametrize("nbytes,src_off,dst_off", [(150_000_013, 0, 16), (1 << 20, 16, 32), (4099, 3, 0),
+                                                    (15, 0, 0)])
+def test_device_copy_sizes(gpu, nbytes, src_off, dst_off):
+    """h3_buffer_copy at large, aligned, misaligned and tiny sizes: the destination range equals the source and
+    the bytes around it stay untouched."""
+    rng = np.random.default_rng(nbytes)
+    a = rng.integers(0, 256, nbytes + src_off, dtype=np.uint8)
+    A = gpu.upload(a, "u8")
+    B = gpu.upload(np.full(nbytes + dst_off + 64, 0xA5, np.uint8), "u8")
+    print(f"[copy] bytes={nbytes} src_off={src_off} dst_off={dst_off}", flush=True)
+    A.view((nbytes,), offset_elems=src_off).copy_to(B.view((nbytes,), offset_elems=dst_off))
+    got = B.numpy()
+    assert np.array_equal(got[dst_off:dst_off + nbytes], a[src_off:])
+    assert (got[:dst_off] == 0xA5).all() and (got[dst_off + nbytes:] == 0xA5).all()
+
+
 def test_misaligned_views_refused(gpu):
     """Q/K/V rows are read 16 bytes at a time and O written 4 elements at a time: a view whose base breaks
     that is refused on the host, not run."""
