@@ -490,7 +490,9 @@ void attention_wave_kernel(const char *__restrict__ Q, const char *__restrict__ 
         const int i = 4 * g + e;
         const VP2 pp = {(VE)xv[i], (VE)xv[i + 1]};
         pb[t][u][i >> 3][(i & 7) >> 1] = __builtin_bit_cast(int, pp);
+#ifndef WAVE_NO_SUM
         la[(g & 1) * 2 + (e >> 1)] = sum2<VT>(pp, la[(g & 1) * 2 + (e >> 1)]);
+#endif
       }
     };
 #define SB __builtin_amdgcn_sched_barrier(0)
